@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Verify + commit benchmark for one GDN layer on one MI355X.
+
+One step = ``gdn_recoverssm_verify`` over the whole speculative batch, then the
+commit of the accepted prefix (``GDNRecoverSSMCommitContext.commit``: plan +
+fold, conv compaction timed separately) on the align-mode workload
+``align_b256``: 256 sequences, 16 key / 32 value heads, K = V = 128, Q = 4, FP32
+state pages, bf16 activations, block size 64 with ~25% of the rows crossing a
+block boundary, accepted lengths uniform in {0..4}, 6 padded rows.
+
+``value`` is the achieved HBM bandwidth of the step: algorithmic bytes (the
+byte model below, computed from the seeded draws) divided by the measured step
+time, with every input resident in HBM before the timed region starts.
+Per-kernel durations come from HIP events on the stream the kernels run on.
+
+Algorithmic bytes (f32 state, bf16 activations / keys):
+  verify = B_valid*HV*V*K*4 (state, once)  + T*(2*H*K + HV*V)*2 (q, k, v)
+         + T*HV*8 (g, beta) + (2B+1)*4 (offsets, slots) + T*HV*V*2 (out)
+         + T*HV*V*4 (corrections) + T*H*K*2 (keys) + T*HV*4 (decays)
+         + T_null*HV*V*2 (zero outputs of padded rows)
+  commit = sum over rows with n > 0 of HV*V*K*4*(2 + boundary written)
+         + n*(HV*V*4 + H*K*2 + HV*4)  + 52*B (plan reads and writes)
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "gdn-recoverssm-ascend_amd"))
+
+METRIC = "verify+commit HBM GB/s (% of peak) + µs/spec step, GDN layer B=256 Q=4"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="align_b256")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true", help="skip the per-kernel event pass")
+    ap.add_argument("--copy-calibration", type=int, default=0,
+                    help="also run a device copy of this many MiB (PMC scale calibration)")
+    return ap.parse_args()
+
+
+def byte_model(w, plan_lens, plan_final, plan_boundary, plan_blen):
+    import torch
+
+    s = w.spec
+    B, HV, H, K, V = s.rows, s.value_heads, s.key_heads, s.key_dim, s.value_dim
+    qsl = w.meta.query_start_loc.cpu().long()
+    qlen = (qsl[1:] - qsl[:-1]).clamp(min=0, max=s.window)
+    idx = w.meta.state_indices.cpu().long()
+    valid = (idx > 0) & (idx < w.num_pages)
+    T = int(qlen[valid].sum())
+    T_null = int(qlen[~valid].sum())
+    verify = (
+        int(valid.sum()) * HV * V * K * 4
+        + T * (2 * H * K + HV * V) * 2
+        + T * HV * 8
+        + (2 * B + 1) * 4
+        + T * HV * V * 2
+        + T * HV * V * 4
+        + T * H * K * 2
+        + T * HV * 4
+        + T_null * HV * V * 2
+    )
+    n = plan_lens.cpu().long()[:B]
+    fin = plan_final.cpu().long()[:B]
+    bnd = plan_boundary.cpu().long()[:B]
+    blen = plan_blen.cpu().long()[:B]
+    active = n > 0
+    store_b = active & (bnd > 0) & (bnd < w.num_pages) & (bnd != fin) & (blen > 0) & (blen <= n)
+    state_pages = int(active.sum()) * 2 + int(store_b.sum())
+    commit = state_pages * HV * V * K * 4 + int(n[active].sum()) * (HV * V * 4 + H * K * 2 + HV * 4) + 52 * B
+    return dict(verify=verify, commit=commit, tokens=T, active_rows=int(active.sum()),
+                boundary_writes=int(store_b.sum()), accepted_tokens=int(n[active].sum()))
+
+
+def cpu_baseline(w_cpu, threads):
+    """FP32 torch oracle on the host cores: one full verify + plan + fold step."""
+    import torch
+
+    sys.path.insert(0, os.path.join(HERE, "oracle"))
+    import gdn_oracle as O
+
+    torch.set_num_threads(threads)
+    s = w_cpu.spec
+    inp = w_cpu.inputs[0]
+    m = w_cpu.meta
+    t0 = time.perf_counter()
+    res = O.oracle_verify(inp.q, inp.k, inp.v, inp.g, inp.beta, w_cpu.checkpoints[0], m.query_start_loc,
+                          m.state_indices, s.window, dtype=torch.float32)
+    plan = O.oracle_plan_single(m.accepted, m.state_indices, m.query_start_loc, spec_query_len=s.window,
+                                num_blocks=w_cpu.num_pages, block_table=m.block_table, num_computed=m.num_computed,
+                                block_size=m.block_size)
+    O.oracle_fold([w_cpu.checkpoints[0]], [res.correction], [res.key], [res.decay], source=m.state_indices,
+                  lengths=plan["commit_lens"], final=plan["final"], boundary=plan["boundary"],
+                  boundary_len=plan["boundary_len"], rows=s.rows, num_blocks=w_cpu.num_pages, record_rows=s.rows,
+                  dtype=torch.float32)
+    return time.perf_counter() - t0
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
+              "(the verify/commit path shards by rows and heads with no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+    import torch
+
+    from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    want_cpu = not args.no_cpu_baseline
+    w_cpu = W.make_workload(args.workload) if want_cpu else None
+    w = w_cpu.to(dev) if want_cpu else W.make_workload(args.workload, gen_device="cuda").to(dev)
+    s = w.spec
+    B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+    inp = w.inputs[0]
+    rec = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype)
+    ctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, [rec], spec_query_len=Q, max_num_reqs=B)
+    out = torch.empty(1, w.tokens, HV, V, dtype=inp.v.dtype, device=dev)
+    m = w.meta
+    align = m.block_table is not None
+    verify_specs: list = []
+    gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0], replay_cache=rec,
+                          query_start_loc=m.query_start_loc, state_indices=m.state_indices, spec_query_len=Q, out=out,
+                          _collect=verify_specs)
+    commit_specs = ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
+                                         block_table=m.block_table if align else None,
+                                         num_computed_tokens=m.num_computed if align else None,
+                                         mamba_block_size=m.block_size if align else None, commit_conv=True)
+    by_name = {sp.name: sp for sp in commit_specs}
+    step_specs = verify_specs + [by_name["plan"], by_name["fold"]]
+
+    def step():
+        for sp in step_specs:
+            sp.launch()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t_start.elapsed_time(t_end) / args.steps
+
+    # Per-kernel durations (HIP events around each launch on the same stream).
+    kernel_ms = {}
+    if not args.kernel_only:
+        reps = max(10, args.steps // 2)
+        for sp in step_specs + [by_name["conv"]]:
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for a, b in ev:
+                a.record(stream)
+                sp.launch()
+                b.record(stream)
+            torch.cuda.synchronize()
+            kernel_ms[sp.name] = sum(a.elapsed_time(b) for a, b in ev) / reps
+
+    nbytes = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
+    total = nbytes["verify"] + nbytes["commit"]
+    gbs = total / (step_ms * 1e-3) / 1e9
+
+    per_kernel = {}
+    for name, ms in kernel_ms.items():
+        b = {"verify": nbytes["verify"], "fold": nbytes["commit"] - 52 * B, "plan": 52 * B}.get(name)
+        entry = {"us": round(ms * 1e3, 2)}
+        if b is not None:
+            entry.update(bytes=b, gbs=round(b / (ms * 1e-3) / 1e9, 1), frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        per_kernel[name] = entry
+    dominant = max(("verify", "fold"), key=lambda n: kernel_ms.get(n, 0.0)) if kernel_ms else "fold"
+    dk = per_kernel.get(dominant, {})
+    roofline = {
+        "kernel": dominant,
+        "bound": "hbm",
+        "achieved": dk.get("gbs"),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": dk.get("frac"),
+        "traffic": None,
+        "algorithmic_bytes": dk.get("bytes"),
+        "avg_us": dk.get("us"),
+    }
+
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        a = torch.ones(n, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+
+    cpu = None
+    if want_cpu:
+        threads = max(1, min(os.cpu_count() or 1, 16))
+        secs = cpu_baseline(w_cpu, threads)
+        cpu = {
+            "value": round(total / secs / 1e9, 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"one full verify+plan+fold step of {s.name} (all {B} rows) with the FP32 torch oracle; "
+                      f"{secs * 1e3:.0f} ms/step",
+            "ms_per_step": round(secs * 1e3, 1),
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "us_per_step": round(step_ms * 1e3, 2),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": s.name, "rows": B, "key_heads": H, "value_heads": HV, "key_dim": K, "value_dim": V,
+            "window": Q, "mode": "align" if align else "none", "block_size": m.block_size,
+            "state": "f32", "activations": "bf16", "key_records": "bf16",
+        },
+        "bytes": {**nbytes, "step": total},
+        "kernels": per_kernel,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

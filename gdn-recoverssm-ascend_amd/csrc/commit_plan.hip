@@ -1,0 +1,344 @@
+// Commit plan, conv-state compaction and align publication: the integer /
+// byte-copy parts of the post-sampling commit. One thread per spec row (plan,
+// publication) or per (layer, row, channel) (compaction).
+//
+// Plan semantics: grouped_commit.py:109-222 (grouped) and kernels.py:975-1072
+// (single context). Every index derived from data is bounds-checked against the
+// sizes the host passes; an out-of-range index makes the row a no-op (the
+// reference would read outside the tensor there).
+#include "gdn_common.cuh"
+
+namespace gdn {
+
+struct PlanArgs {
+  const void *sampled;
+  int64_t sampled_stride, sampled_len;
+  int32_t sampled_dtype, num_groups;
+  gdn_plan_group groups[GDN_PLAN_MAX_GROUPS];
+  int32_t *source, *lens, *final_, *boundary, *boundary_lens, *valid, *col;
+  const void *idx_mapping;
+  int64_t idx_len;
+  int32_t idx_dtype;
+  uint32_t flags;
+  int32_t *pcols, *pacc;
+  int64_t plen, rows, cap, null_block, Q;
+};
+
+// Division with truncation toward zero, as the reference kernels' integer `//`.
+__device__ __forceinline__ int64_t tdiv(int64_t a, int64_t b) { return a / b; }
+
+__global__ __launch_bounds__(64) void plan_kernel(PlanArgs a) {
+  const int64_t row = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= a.rows) return;
+  const bool align = (a.flags & GDN_PLAN_ALIGN) != 0;
+  const bool grouped = (a.flags & GDN_PLAN_GROUPED) != 0;
+  const int64_t null_block = a.null_block;
+  bool all_valid = true;
+  int64_t shared_col = -1, shared_request = -1;
+  for (int gi = 0; gi < a.num_groups; ++gi) {
+    const gdn_plan_group &g = a.groups[gi];
+    const int64_t request = g.request_indices ? load_index(g.request_indices, row * g.map_stride, g.map_dtype) : row;
+    const int64_t source = load_index(g.state_indices, row * g.si_stride, g.si_dtype);
+    const int64_t bos = load_index(g.query_start_loc, row * g.qsl_stride, g.qsl_dtype);
+    const int64_t eos = load_index(g.query_start_loc, (row + 1) * g.qsl_stride, g.qsl_dtype);
+    const int64_t qlen = eos - bos;
+    bool request_ok = request >= 0 && request < a.sampled_len;
+    if (align) request_ok = request_ok && request < g.table_rows && request < g.computed_len;
+    const int64_t accepted =
+        request_ok ? int64_t(int32_t(load_index(a.sampled, request * a.sampled_stride, a.sampled_dtype))) : 0;
+    int64_t count = min(max(accepted, int64_t(0)), qlen);
+    count = min(count, a.Q);
+    int64_t final_idx = source, boundary = null_block, blen = 0, col = 0;
+    bool computed_ok = true;
+    if (align && request_ok) {
+      const int64_t C =
+          int64_t(int32_t(load_index(g.num_computed, request * g.computed_stride, g.computed_dtype)));
+      computed_ok = C >= 0;
+      const int64_t position = C + count;
+      col = min(tdiv(max(position - 1, int64_t(0)), g.block_size), g.table_width - 1);
+      final_idx = load_index(g.block_table, request * g.table_row_stride + col * g.table_col_stride, g.table_dtype);
+      const int64_t next_boundary = (tdiv(C, g.block_size) + 1) * g.block_size;
+      const bool crossed = position >= next_boundary;
+      blen = next_boundary - C;
+      const int64_t bcol = tdiv(next_boundary, g.block_size) - 1;
+      bool load_b = crossed && bcol >= 0 && bcol < g.table_width;
+      if (grouped) load_b = load_b && computed_ok;
+      boundary = load_b ? load_index(g.block_table, request * g.table_row_stride + bcol * g.table_col_stride,
+                                     g.table_dtype)
+                        : null_block;
+    }
+    const bool geometry = bos >= 0 && bos <= eos && qlen <= a.Q;
+    const bool valid = request_ok && geometry && source > null_block && source < g.num_blocks &&
+                       final_idx > null_block && final_idx < g.num_blocks && count > 0 && count <= qlen &&
+                       computed_ok;
+    const bool boundary_ok = boundary > null_block && boundary < g.num_blocks;
+    if (align && !boundary_ok) blen = 0;
+    if (grouped && !boundary_ok) boundary = null_block;
+    const int64_t off = int64_t(gi) * a.cap + row;
+    if (a.source) a.source[off] = int32_t(valid ? source : null_block);
+    a.lens[off] = int32_t(valid ? count : 0);
+    a.final_[off] = int32_t(valid ? final_idx : null_block);
+    a.boundary[off] = int32_t(valid ? boundary : null_block);
+    a.boundary_lens[off] = int32_t(valid ? blen : 0);
+    if (a.valid) a.valid[off] = valid ? 1 : 0;
+    if (a.col) a.col[off] = int32_t(col);
+    if (gi == 0) {
+      shared_col = col;
+      shared_request = request;
+    } else {
+      all_valid = all_valid && col == shared_col && request == shared_request;
+    }
+    all_valid = all_valid && valid;
+  }
+  if ((a.flags & GDN_PLAN_PUBLISH) && align) {
+    if (shared_request >= 0 && shared_request < a.idx_len) {
+      const int64_t slot = load_index(a.idx_mapping, shared_request, a.idx_dtype);
+      if (all_valid && slot >= 0 && slot < a.plen) {
+        a.pcols[slot] = int32_t(shared_col);
+        a.pacc[slot] = 1;
+      }
+    }
+  }
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void conv_compact_kernel(
+    const int64_t *__restrict__ addrs, const int64_t *__restrict__ block_strides,
+    const int64_t *__restrict__ dim_strides, const int64_t *__restrict__ token_strides, const void *source,
+    int32_t source_dtype, int64_t source_stride, const int32_t *__restrict__ lengths,
+    const int32_t *__restrict__ finals, const int32_t *__restrict__ boundaries,
+    const int32_t *__restrict__ boundary_lens, const int32_t *__restrict__ layer_groups, int64_t cap,
+    int64_t null_block, int64_t rows, int64_t conv_dim, int64_t history, int64_t window, int64_t num_blocks,
+    int32_t align, int64_t dim_tiles) {
+  const int64_t wg = blockIdx.x;
+  const int64_t tile = wg % dim_tiles;
+  const int64_t row = (wg / dim_tiles) % rows;
+  const int64_t layer = wg / (dim_tiles * rows);
+  const int64_t d = tile * blockDim.x + threadIdx.x;
+  if (d >= conv_dim) return;
+  const int64_t plan_row = (layer_groups ? int64_t(layer_groups[layer]) * cap : 0) + row;
+  const int64_t src = load_index(source, plan_row * source_stride, source_dtype);
+  const int64_t n = lengths[plan_row];
+  const int64_t fin = finals[plan_row];
+  if (!(src > null_block && src < num_blocks && n >= 1 && n - 1 + history <= window && fin > null_block &&
+        fin < num_blocks))
+    return;
+  E *base = reinterpret_cast<E *>(addrs[layer]);
+  const int64_t bs = block_strides[layer], ds = dim_strides[layer], ts = token_strides[layer];
+  const E *sp = base + src * bs + d * ds;
+  constexpr int kMaxHist = 16;
+  E fv[kMaxHist], bv[kMaxHist];
+  const int64_t hist = history;  // host checks history <= kMaxHist
+  for (int64_t h = 0; h < hist; ++h) fv[h] = sp[(n - 1 + h) * ts];
+  bool store_b = false;
+  int64_t bidx = null_block;
+  if (align) {
+    bidx = boundaries[plan_row];
+    const int64_t blen = boundary_lens[plan_row];
+    store_b = bidx > null_block && bidx < num_blocks && blen >= 1 && blen - 1 + history <= window;
+    if (store_b)
+      for (int64_t h = 0; h < hist; ++h) bv[h] = sp[(blen - 1 + h) * ts];
+  }
+  if (store_b) {
+    E *bp = base + bidx * bs + d * ds;
+    for (int64_t h = 0; h < hist; ++h) bp[h * ts] = bv[h];
+  }
+  E *fp = base + fin * bs + d * ds;
+  for (int64_t h = 0; h < hist; ++h) fp[h * ts] = fv[h];
+}
+
+__global__ __launch_bounds__(64) void publish_kernel(const int64_t *__restrict__ desc, int64_t num_buckets,
+                                                     const void *request_indices, int32_t request_dtype,
+                                                     int64_t request_stride, const void *idx_mapping,
+                                                     int32_t idx_dtype, int64_t idx_len, int32_t *pcols,
+                                                     int32_t *pacc, int64_t plen, int64_t rows) {
+  const int64_t row = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const int32_t *first_cols = reinterpret_cast<const int32_t *>(desc[1]);
+  const int32_t shared_col = first_cols[row];
+  bool valid = true;
+  for (int64_t b = 0; b < num_buckets; ++b) {
+    const int32_t *vp = reinterpret_cast<const int32_t *>(desc[4 * b]);
+    const int32_t *cp = reinterpret_cast<const int32_t *>(desc[4 * b + 1]);
+    const int64_t cap = desc[4 * b + 2];
+    const int64_t groups = desc[4 * b + 3];
+    for (int64_t g = 0; g < groups; ++g) {
+      const int64_t off = g * cap + row;
+      valid = valid && vp[off] != 0 && cp[off] == shared_col;
+    }
+  }
+  const int64_t request = load_index(request_indices, row * request_stride, request_dtype);
+  if (request < 0 || request >= idx_len) return;
+  const int64_t slot = load_index(idx_mapping, request, idx_dtype);
+  if (valid && slot >= 0 && slot < plen) {
+    pcols[slot] = shared_col;
+    pacc[slot] = 1;
+  }
+}
+
+static bool index_dtype_ok(int32_t dt) { return dt == GDN_DT_I32 || dt == GDN_DT_I64; }
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, int64_t sampled_stride,
+                                   int64_t sampled_len, const gdn_plan_group *groups, int32_t num_groups,
+                                   int32_t *source_plan, int32_t *lens_plan, int32_t *final_plan,
+                                   int32_t *boundary_plan, int32_t *boundary_lens_plan, int32_t *valid_plan,
+                                   int32_t *col_plan, const void *idx_mapping, int32_t idx_mapping_dtype,
+                                   int64_t idx_mapping_len, int32_t *persistent_cols, int32_t *persistent_accepted,
+                                   int64_t persistent_len, int64_t num_rows, int64_t plan_capacity,
+                                   int64_t null_block, int64_t spec_query_len, uint32_t flags, void *stream) {
+  if (num_groups < 1 || num_groups > GDN_PLAN_MAX_GROUPS) {
+    set_error("plan: num_groups=%d outside [1, %d]", num_groups, GDN_PLAN_MAX_GROUPS);
+    return GDN_ERR_INVALID;
+  }
+  if (num_rows < 0 || num_rows > plan_capacity || plan_capacity <= 0) {
+    set_error("plan: rows=%lld outside plan capacity %lld", (long long)num_rows, (long long)plan_capacity);
+    return GDN_ERR_INVALID;
+  }
+  if (spec_query_len < 1 || spec_query_len > 8) {
+    set_error("plan: spec_query_len=%lld outside [1, 8]", (long long)spec_query_len);
+    return GDN_ERR_INVALID;
+  }
+  if (!sampled || !index_dtype_ok(sampled_dtype) || sampled_len < 0 || !lens_plan || !final_plan ||
+      !boundary_plan || !boundary_lens_plan) {
+    set_error("plan: missing accepted counts or plan outputs");
+    return GDN_ERR_INVALID;
+  }
+  const bool align = flags & GDN_PLAN_ALIGN;
+  const bool grouped = flags & GDN_PLAN_GROUPED;
+  if (grouped && !source_plan) {
+    set_error("plan: grouped plans store the source");
+    return GDN_ERR_INVALID;
+  }
+  if ((flags & GDN_PLAN_PUBLISH) && align &&
+      (!idx_mapping || !persistent_cols || !persistent_accepted || !index_dtype_ok(idx_mapping_dtype))) {
+    set_error("plan: publication needs idx_mapping and the persistent outputs");
+    return GDN_ERR_INVALID;
+  }
+  PlanArgs a{};
+  a.sampled = sampled;
+  a.sampled_stride = sampled_stride;
+  a.sampled_len = sampled_len;
+  a.sampled_dtype = sampled_dtype;
+  a.num_groups = num_groups;
+  for (int i = 0; i < num_groups; ++i) {
+    const gdn_plan_group &g = groups[i];
+    if (!g.state_indices || !g.query_start_loc || !index_dtype_ok(g.si_dtype) || !index_dtype_ok(g.qsl_dtype) ||
+        (g.request_indices && !index_dtype_ok(g.map_dtype))) {
+      set_error("plan: group %d lacks state indices / offsets or has a non-integer dtype", i);
+      return GDN_ERR_INVALID;
+    }
+    if (align && (!g.block_table || !g.num_computed || g.block_size <= 0 || g.table_width <= 0 ||
+                  !index_dtype_ok(g.table_dtype) || !index_dtype_ok(g.computed_dtype))) {
+      set_error("plan: group %d align metadata incomplete", i);
+      return GDN_ERR_INVALID;
+    }
+    a.groups[i] = g;
+  }
+  a.source = source_plan;
+  a.lens = lens_plan;
+  a.final_ = final_plan;
+  a.boundary = boundary_plan;
+  a.boundary_lens = boundary_lens_plan;
+  a.valid = valid_plan;
+  a.col = col_plan;
+  a.idx_mapping = idx_mapping;
+  a.idx_len = idx_mapping ? idx_mapping_len : 0;
+  a.idx_dtype = idx_mapping_dtype;
+  a.flags = flags;
+  a.pcols = persistent_cols;
+  a.pacc = persistent_accepted;
+  a.plen = persistent_len;
+  a.rows = num_rows;
+  a.cap = plan_capacity;
+  a.null_block = null_block;
+  a.Q = spec_query_len;
+  if (num_rows == 0) return GDN_OK;
+  const unsigned blocks = unsigned((num_rows + 63) / 64);
+  hipLaunchKernelGGL(plan_kernel, dim3(blocks), dim3(64), 0, static_cast<hipStream_t>(stream), a);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("plan: launch failed: %s", hipGetErrorString(err));
+    return GDN_ERR_LAUNCH;
+  }
+  return GDN_OK;
+}
+
+extern "C" int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int64_t *conv_block_strides,
+                                           const int64_t *conv_dim_strides, const int64_t *conv_token_strides,
+                                           const void *source, int32_t source_dtype, int64_t source_stride,
+                                           const int32_t *lengths, const int32_t *final_indices,
+                                           const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                                           const int32_t *layer_groups, int64_t plan_capacity,
+                                           int64_t null_block, int64_t num_rows, int64_t num_layers,
+                                           int64_t conv_dim, int64_t history, int64_t window, int64_t num_blocks,
+                                           int32_t element_bytes, int32_t align, void *stream) {
+  if (!conv_addrs || !conv_block_strides || !conv_dim_strides || !conv_token_strides || !source || !lengths ||
+      !final_indices || !boundary_indices || !boundary_lengths || !index_dtype_ok(source_dtype)) {
+    set_error("conv_compact: missing table or plan pointer");
+    return GDN_ERR_INVALID;
+  }
+  if (history < 1 || history > 16 || window < history || conv_dim < 1 || num_layers < 1 || num_rows < 0) {
+    set_error("conv_compact: history=%lld window=%lld dim=%lld layers=%lld unsupported", (long long)history,
+              (long long)window, (long long)conv_dim, (long long)num_layers);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (element_bytes != 2 && element_bytes != 4) {
+    set_error("conv_compact: element size %d unsupported", element_bytes);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (num_rows == 0) return GDN_OK;
+  const int64_t tiles = (conv_dim + 255) / 256;
+  const int64_t grid = tiles * num_rows * num_layers;
+  if (grid > 0x7fffffffLL) {
+    set_error("conv_compact: grid too large");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  auto s = static_cast<hipStream_t>(stream);
+  if (element_bytes == 2)
+    hipLaunchKernelGGL(conv_compact_kernel<uint16_t>, dim3(unsigned(grid)), dim3(256), 0, s, conv_addrs,
+                       conv_block_strides, conv_dim_strides, conv_token_strides, source, source_dtype,
+                       source_stride, lengths, final_indices, boundary_indices, boundary_lengths, layer_groups,
+                       plan_capacity, null_block, num_rows, conv_dim, history, window, num_blocks, align, tiles);
+  else
+    hipLaunchKernelGGL(conv_compact_kernel<uint32_t>, dim3(unsigned(grid)), dim3(256), 0, s, conv_addrs,
+                       conv_block_strides, conv_dim_strides, conv_token_strides, source, source_dtype,
+                       source_stride, lengths, final_indices, boundary_indices, boundary_lengths, layer_groups,
+                       plan_capacity, null_block, num_rows, conv_dim, history, window, num_blocks, align, tiles);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("conv_compact: launch failed: %s", hipGetErrorString(err));
+    return GDN_ERR_LAUNCH;
+  }
+  return GDN_OK;
+}
+
+extern "C" int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_buckets, const void *request_indices,
+                                      int32_t request_dtype, int64_t request_stride, int64_t request_len,
+                                      const void *idx_mapping, int32_t idx_mapping_dtype, int64_t idx_mapping_len,
+                                      int32_t *persistent_cols, int32_t *persistent_accepted,
+                                      int64_t persistent_len, int64_t num_rows, void *stream) {
+  if (!descriptors || num_buckets < 1 || !request_indices || !idx_mapping || !persistent_cols ||
+      !persistent_accepted || !index_dtype_ok(request_dtype) || !index_dtype_ok(idx_mapping_dtype)) {
+    set_error("publish: missing descriptor, mapping or persistent output");
+    return GDN_ERR_INVALID;
+  }
+  if (num_rows < 0 || num_rows > request_len) {
+    set_error("publish: rows exceed the request mapping");
+    return GDN_ERR_INVALID;
+  }
+  if (num_rows == 0) return GDN_OK;
+  const unsigned blocks = unsigned((num_rows + 63) / 64);
+  hipLaunchKernelGGL(publish_kernel, dim3(blocks), dim3(64), 0, static_cast<hipStream_t>(stream), descriptors,
+                     num_buckets, request_indices, request_dtype, request_stride, idx_mapping, idx_mapping_dtype,
+                     idx_mapping_len, persistent_cols, persistent_accepted, persistent_len, num_rows);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("publish: launch failed: %s", hipGetErrorString(err));
+    return GDN_ERR_LAUNCH;
+  }
+  return GDN_OK;
+}

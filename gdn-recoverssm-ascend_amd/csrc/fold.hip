@@ -1,0 +1,265 @@
+// Commit fold: replays the accepted prefix of the verify records into each
+// layer's checkpoint in place (grouped_commit.py:377-480, kernels.py:1222-1324,
+// csrc/fold.h:192-237 of the reference plugin).
+//
+// One workgroup (256 threads) owns one (layer, row, value head) state [V, K].
+// The state is streamed once: each thread loads 16-byte chunks of its rows
+// (consecutive threads -> consecutive chunks, so every wave instruction covers
+// whole 128-byte lines), folds
+//     h <- fma(c_t, k_t, h * decay_t),   t = 0 .. n-1
+// in registers, stores the boundary snapshot after `boundary_len` tokens and
+// the final state after n tokens. Every chunk a thread stores was loaded by the
+// same thread before its first store, so source / final / boundary pages may
+// alias. Corrections and keys of the accepted tokens are staged in LDS.
+#include "gdn_common.cuh"
+
+namespace gdn {
+
+struct FoldArgs {
+  const int64_t *state_addrs, *state_bs, *corr_addrs, *corr_bs, *key_addrs, *key_bs, *decay_addrs, *decay_bs;
+  const int32_t *layer_groups;
+  const void *source;
+  const int32_t *lengths, *finals, *boundaries, *boundary_lens;
+  int64_t source_stride;
+  int64_t rows, heads, ratio, Q, blocks, record_rows, cap, null_block;
+  int64_t state_head_stride, state_v_stride;
+  int64_t corr_head_stride, corr_token_stride;
+  int64_t key_head_stride, key_token_stride;
+  int64_t decay_head_stride, decay_token_stride;
+  int32_t K, V, KP, KCH;  // KP: K padded to a whole number of chunks; KCH = KP / E
+  int32_t source_dtype;
+};
+
+constexpr int kFoldThreads = 256;
+
+template <typename S, typename KT>
+__global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
+  constexpr int E = Chunk<S>::E;
+  constexpr int ITERS = 64 / E;  // chunks held per thread per batch (64 f32 values)
+  extern __shared__ float lds[];
+
+  const int64_t w = blockIdx.x;
+  const int64_t hv = w % a.heads;
+  const int64_t row = (w / a.heads) % a.rows;
+  const int64_t layer = w / (a.heads * a.rows);
+  const int64_t plan_row = (a.layer_groups ? int64_t(a.layer_groups[layer]) * a.cap : 0) + row;
+  const int64_t src = load_index(a.source, plan_row * a.source_stride, a.source_dtype);
+  const int n = a.lengths[plan_row];
+  const int64_t fin = a.finals[plan_row];
+  if (!(src > a.null_block && src < a.blocks && n > 0 && n <= a.Q && fin > a.null_block && fin < a.blocks &&
+        row < a.record_rows))
+    return;
+  const int64_t bidx = a.boundaries[plan_row];
+  const int blen = a.boundary_lens[plan_row];
+  const bool store_b = bidx > a.null_block && bidx < a.blocks && bidx != fin && blen > 0 && blen <= n;
+
+  S *base = reinterpret_cast<S *>(a.state_addrs[layer]);
+  const int64_t sbs = a.state_bs[layer];
+  const S *src_p = base + src * sbs + hv * a.state_head_stride;
+  S *fin_p = base + fin * sbs + hv * a.state_head_stride;
+  S *bnd_p = base + (store_b ? bidx : fin) * sbs + hv * a.state_head_stride;
+
+  const int tid = threadIdx.x;
+  const int KCH = a.KCH;
+  const int kc = tid % KCH;
+  const int r0 = tid / KCH;
+  const int RP = kFoldThreads / KCH;  // rows covered by one pass of the workgroup
+  const bool kc_ok = kc * E < a.K;
+  const int V = a.V;
+  const int64_t vs = a.state_v_stride;
+
+  // Issue the first batch of state loads before staging the records.
+  uint4 raw[ITERS];
+#pragma unroll
+  for (int i = 0; i < ITERS; ++i) {
+    const int r = r0 + i * RP;
+    raw[i] = (r < V && kc_ok) ? *reinterpret_cast<const uint4 *>(src_p + r * vs + kc * E) : make_uint4(0, 0, 0, 0);
+  }
+
+  float *corr_lds = lds;                    // [n][V]
+  float *key_lds = lds + a.Q * V;           // [n][KP]
+  const float *corr_base = reinterpret_cast<const float *>(a.corr_addrs[layer]) + row * a.corr_bs[layer] +
+                           hv * a.corr_head_stride;
+  const KT *key_base = reinterpret_cast<const KT *>(a.key_addrs[layer]) + row * a.key_bs[layer] +
+                       (hv / a.ratio) * a.key_head_stride;
+  const float *decay_base = reinterpret_cast<const float *>(a.decay_addrs[layer]) + row * a.decay_bs[layer] +
+                            hv * a.decay_head_stride;
+  for (int idx = tid; idx < n * V; idx += kFoldThreads) {
+    const int t = idx / V, v = idx - t * V;
+    corr_lds[t * V + v] = corr_base[t * a.corr_token_stride + v];
+  }
+  const int KP = a.KP;
+  for (int idx = tid; idx < n * KP; idx += kFoldThreads) {
+    const int t = idx / KP, k = idx - t * KP;
+    key_lds[t * KP + k] = k < a.K ? to_f32(key_base[t * a.key_token_stride + k]) : 0.0f;
+  }
+  float decay[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) decay[t] = t < n ? decay_base[t * a.decay_token_stride] : 1.0f;
+  __syncthreads();
+
+  const int passes = (V + RP - 1) / RP;
+  for (int first = 0; first < passes; first += ITERS) {
+    if (first > 0) {
+#pragma unroll
+      for (int i = 0; i < ITERS; ++i) {
+        const int r = r0 + (first + i) * RP;
+        raw[i] = (r < V && kc_ok) ? *reinterpret_cast<const uint4 *>(src_p + r * vs + kc * E) : make_uint4(0, 0, 0, 0);
+      }
+    }
+    float h[ITERS][E];
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) unpack16<S>(raw[i], h[i]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t < n) {
+        float kv[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) kv[e] = key_lds[t * KP + kc * E + e];
+        const float d = decay[t];
+#pragma unroll
+        for (int i = 0; i < ITERS; ++i) {
+          const int r = r0 + (first + i) * RP;
+          const float c = corr_lds[t * V + (r < V ? r : 0)];
+#pragma unroll
+          for (int e = 0; e < E; ++e) h[i][e] = __builtin_fmaf(c, kv[e], h[i][e] * d);
+        }
+        if (store_b && t + 1 == blen) {
+#pragma unroll
+          for (int i = 0; i < ITERS; ++i) {
+            const int r = r0 + (first + i) * RP;
+            if (r < V && kc_ok) *reinterpret_cast<uint4 *>(bnd_p + r * vs + kc * E) = pack16<S>(h[i]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) {
+      const int r = r0 + (first + i) * RP;
+      if (r < V && kc_ok) *reinterpret_cast<uint4 *>(fin_p + r * vs + kc * E) = pack16<S>(h[i]);
+    }
+  }
+}
+
+template <typename S>
+static void launch_fold_key(int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a) {
+  switch (key_dtype) {
+    case GDN_DT_BF16: hipLaunchKernelGGL((fold_kernel<S, bf16>), grid, dim3(kFoldThreads), lds, s, a); break;
+    case GDN_DT_F16: hipLaunchKernelGGL((fold_kernel<S, f16>), grid, dim3(kFoldThreads), lds, s, a); break;
+    default: hipLaunchKernelGGL((fold_kernel<S, float>), grid, dim3(kFoldThreads), lds, s, a); break;
+  }
+}
+
+static bool float_dtype_ok(int32_t dt) { return dt == GDN_DT_F32 || dt == GDN_DT_BF16 || dt == GDN_DT_F16; }
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, const void *key_ref,
+                                   const void *decay_ref, const int64_t *state_addrs,
+                                   const int64_t *state_block_strides, const int64_t *corr_addrs,
+                                   const int64_t *corr_block_strides, const int64_t *key_addrs,
+                                   const int64_t *key_block_strides, const int64_t *decay_addrs,
+                                   const int64_t *decay_block_strides, const int32_t *layer_groups,
+                                   const void *source, const int32_t *lengths, const int32_t *final_indices,
+                                   const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                                   const int64_t *config, int64_t config_len, const gdn_fold_ext *ext,
+                                   void *stream) {
+  (void)state_ref;
+  (void)correction_ref;
+  (void)key_ref;
+  (void)decay_ref;
+  if (!config || config_len != GDN_FOLD_CONFIG_FIELDS || !ext) {
+    set_error("fold: tiling ABI expects %d config fields and an extension block", GDN_FOLD_CONFIG_FIELDS);
+    return GDN_ERR_INVALID;
+  }
+  // Field order of the reference's GDN_FOLD_FIELDS (csrc/common.h:37-54).
+  const int64_t rows = config[0], layers = config[1], heads = config[2], key_heads = config[3];
+  const int64_t query_len = config[4], blocks = config[5], record_rows = config[6], cap = config[7];
+  const int64_t null_block = config[8];
+  if (!state_addrs || !state_block_strides || !corr_addrs || !corr_block_strides || !key_addrs ||
+      !key_block_strides || !decay_addrs || !decay_block_strides || !source || !lengths || !final_indices ||
+      !boundary_indices || !boundary_lengths) {
+    set_error("fold: missing address table or plan array");
+    return GDN_ERR_INVALID;
+  }
+  if (layers <= 0 || rows <= 0 || rows > record_rows || rows > cap || cap <= 0 || heads <= 0 || key_heads <= 0 ||
+      heads % key_heads != 0 || query_len <= 0 || query_len > 8 || blocks <= 0 || null_block < 0) {
+    set_error("fold: geometry rows=%lld layers=%lld heads=%lld key_heads=%lld Q=%lld record_rows=%lld cap=%lld",
+              (long long)rows, (long long)layers, (long long)heads, (long long)key_heads, (long long)query_len,
+              (long long)record_rows, (long long)cap);
+    return GDN_ERR_INVALID;
+  }
+  if (!float_dtype_ok(ext->state_dtype) || !float_dtype_ok(ext->key_dtype) ||
+      (ext->source_dtype != GDN_DT_I32 && ext->source_dtype != GDN_DT_I64)) {
+    set_error("fold: unsupported state/key/source dtype");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  const int E = ext->state_dtype == GDN_DT_F32 ? 4 : 8;
+  const int64_t K = ext->key_dim, V = ext->value_dim;
+  if (K < 1 || K > 256 || K % E != 0 || V < 1 || V > 1024 || ext->state_k_stride != 1 ||
+      config[10] % E != 0 || config[9] % E != 0) {
+    set_error("fold: K=%lld V=%lld unsupported (K <= 256 and a multiple of %d, V <= 1024, K contiguous, "
+              "16-byte aligned rows)",
+              (long long)K, (long long)V, E);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  FoldArgs a{};
+  a.state_addrs = state_addrs;
+  a.state_bs = state_block_strides;
+  a.corr_addrs = corr_addrs;
+  a.corr_bs = corr_block_strides;
+  a.key_addrs = key_addrs;
+  a.key_bs = key_block_strides;
+  a.decay_addrs = decay_addrs;
+  a.decay_bs = decay_block_strides;
+  a.layer_groups = layer_groups;
+  a.source = source;
+  a.source_dtype = ext->source_dtype;
+  a.source_stride = ext->source_stride;
+  a.lengths = lengths;
+  a.finals = final_indices;
+  a.boundaries = boundary_indices;
+  a.boundary_lens = boundary_lengths;
+  a.rows = rows;
+  a.heads = heads;
+  a.ratio = heads / key_heads;
+  a.Q = query_len;
+  a.blocks = blocks;
+  a.record_rows = record_rows;
+  a.cap = cap;
+  a.null_block = null_block;
+  a.state_head_stride = config[9];
+  a.state_v_stride = config[10];
+  a.corr_head_stride = config[11];
+  a.corr_token_stride = config[12];
+  a.key_head_stride = config[13];
+  a.key_token_stride = config[14];
+  a.decay_head_stride = config[15];
+  a.decay_token_stride = config[16];
+  a.K = int32_t(K);
+  a.V = int32_t(V);
+  int kch = 1;
+  while (kch * E < K) kch *= 2;
+  a.KCH = kch;
+  a.KP = kch * E;
+  const int64_t grid = layers * rows * heads;
+  if (grid > 0x7fffffffLL) {
+    set_error("fold: grid too large");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  const size_t lds = size_t(query_len) * size_t(V + a.KP) * sizeof(float);
+  auto s = static_cast<hipStream_t>(stream);
+  switch (ext->state_dtype) {
+    case GDN_DT_BF16: launch_fold_key<bf16>(ext->key_dtype, dim3(unsigned(grid)), lds, s, a); break;
+    case GDN_DT_F16: launch_fold_key<f16>(ext->key_dtype, dim3(unsigned(grid)), lds, s, a); break;
+    default: launch_fold_key<float>(ext->key_dtype, dim3(unsigned(grid)), lds, s, a); break;
+  }
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("fold: launch failed: %s", hipGetErrorString(err));
+    return GDN_ERR_LAUNCH;
+  }
+  return GDN_OK;
+}

@@ -1,0 +1,134 @@
+// Shared device helpers for the gfx950 RecoverSSM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gdn_recoverssm_hip.h"
+
+namespace gdn {
+
+// ----------------------------------------------------------------------------
+// Element conversions. bf16 <-> f32 are bit operations (round-to-nearest-even on
+// the way down, NaN kept quiet); f16 uses the hardware conversion.
+// ----------------------------------------------------------------------------
+struct bf16 {
+  uint16_t bits;
+};
+using f16 = _Float16;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return __uint_as_float(uint32_t(x.bits) << 16); }
+__device__ __forceinline__ float to_f32(f16 x) { return float(x); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16{uint16_t((u >> 16) | 0x0040u)};
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16{uint16_t(u >> 16)};
+}
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float x) { return f16(x); }
+
+// Load one element of a runtime-typed tensor as f32 (activations, gates).
+__device__ __forceinline__ float load_as_f32(const void *p, int64_t i, int dt) {
+  switch (dt) {
+    case GDN_DT_BF16: return to_f32(static_cast<const bf16 *>(p)[i]);
+    case GDN_DT_F16: return to_f32(static_cast<const f16 *>(p)[i]);
+    default: return static_cast<const float *>(p)[i];
+  }
+}
+
+// Load one element of a runtime-typed integer tensor as int64.
+__device__ __forceinline__ int64_t load_index(const void *p, int64_t i, int dt) {
+  return dt == GDN_DT_I64 ? static_cast<const int64_t *>(p)[i] : int64_t(static_cast<const int32_t *>(p)[i]);
+}
+
+__device__ __forceinline__ void store_from_f32(void *p, int64_t i, int dt, float x) {
+  switch (dt) {
+    case GDN_DT_BF16: static_cast<bf16 *>(p)[i] = from_f32<bf16>(x); break;
+    case GDN_DT_F16: static_cast<f16 *>(p)[i] = from_f32<f16>(x); break;
+    default: static_cast<float *>(p)[i] = x; break;
+  }
+}
+
+// Elements per 16-byte chunk of state storage.
+template <typename T>
+struct Chunk {
+  static constexpr int E = 16 / int(sizeof(T));
+};
+
+// Unpack one 16-byte chunk into E floats.
+template <typename T>
+__device__ __forceinline__ void unpack16(const uint4 &raw, float *out);
+template <>
+__device__ __forceinline__ void unpack16<float>(const uint4 &raw, float *out) {
+  out[0] = __uint_as_float(raw.x);
+  out[1] = __uint_as_float(raw.y);
+  out[2] = __uint_as_float(raw.z);
+  out[3] = __uint_as_float(raw.w);
+}
+template <>
+__device__ __forceinline__ void unpack16<bf16>(const uint4 &raw, float *out) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void unpack16<f16>(const uint4 &raw, float *out) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = float(__builtin_bit_cast(f16, uint16_t(w[i] & 0xffffu)));
+    out[2 * i + 1] = float(__builtin_bit_cast(f16, uint16_t(w[i] >> 16)));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 pack16(const float *in);
+template <>
+__device__ __forceinline__ uint4 pack16<float>(const float *in) {
+  return make_uint4(__float_as_uint(in[0]), __float_as_uint(in[1]), __float_as_uint(in[2]), __float_as_uint(in[3]));
+}
+template <>
+__device__ __forceinline__ uint4 pack16<bf16>(const float *in) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = uint32_t(from_f32<bf16>(in[2 * i]).bits) | (uint32_t(from_f32<bf16>(in[2 * i + 1]).bits) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+template <>
+__device__ __forceinline__ uint4 pack16<f16>(const float *in) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = uint32_t(__builtin_bit_cast(uint16_t, f16(in[2 * i]))) |
+           (uint32_t(__builtin_bit_cast(uint16_t, f16(in[2 * i + 1]))) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ----------------------------------------------------------------------------
+// Cross-lane sums inside aligned groups of 8 lanes with DPP (no LDS traffic):
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], then row_half_mirror, which pairs
+// lane i with lane 7-i of the same 8-lane half-row.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float dpp_sum8(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));
+  return x;
+}
+
+// Thread-local error message set by the host entry points.
+void set_error(const char *fmt, ...);
+
+}  // namespace gdn

@@ -1,0 +1,97 @@
+"""Ahead-of-time build of the gfx950 HIP library (``libgdn_recoverssm_hip.so``).
+
+``python -m gdn_recoverssm_ascend._build`` (or ``build()``) compiles every
+``csrc/*.hip`` source with hipcc for gfx950 into one shared library placed next
+to this package (``_lib/``), where the ctypes loader finds it. The build is
+in-tree so the artefact travels with the source tree; nothing is JIT-compiled
+at run time.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+PROJECT_DIR = os.path.dirname(PKG_DIR)
+REPO_DIR = os.path.dirname(PROJECT_DIR)
+CSRC_DIR = os.path.join(PROJECT_DIR, "csrc")
+INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+LIB_DIR = os.path.join(PKG_DIR, "_lib")
+LIB_NAME = "libgdn_recoverssm_hip.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+ARCH = os.environ.get("GDN_OFFLOAD_ARCH", "gfx950")
+
+
+def sources() -> list[str]:
+    return sorted(os.path.join(CSRC_DIR, f) for f in os.listdir(CSRC_DIR) if f.endswith(".hip"))
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 HIP library cannot be built")
+
+
+def compile_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-Wall",
+        "-Wno-unused-function",
+        # Packed FP32 instructions stay off: plain FP32 VALU code only.
+        "-Xclang",
+        "-target-feature",
+        "-Xclang",
+        "-packed-fp32-ops",
+        f"-I{INCLUDE_DIR}",
+        f"-I{CSRC_DIR}",
+    ]
+
+
+def build(verbose: bool = False, jobs: int = 4) -> str:
+    """Compile every source (in parallel) and link the shared library."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    cc = hipcc()
+    srcs = sources()
+    with tempfile.TemporaryDirectory(prefix="gdn_build_") as tmp:
+        objs = []
+        procs = []
+        for src in srcs:
+            obj = os.path.join(tmp, os.path.basename(src) + ".o")
+            objs.append(obj)
+            cmd = [cc, *compile_flags(), "-c", src, "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+            if len([p for _, p in procs if p.poll() is None]) >= jobs:
+                procs[0][1].wait()
+        errors = []
+        for src, p in procs:
+            out, _ = p.communicate()
+            text = out.decode(errors="replace")
+            text = "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l and l.strip() != "1 warning generated.")
+            if p.returncode != 0:
+                errors.append(f"{src}:\n{text}")
+            elif verbose and text.strip():
+                print(text)
+        if errors:
+            raise RuntimeError("hipcc failed:\n" + "\n".join(errors))
+        tmp_lib = LIB_PATH + ".tmp"
+        link = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib]
+        r = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        if r.returncode != 0:
+            raise RuntimeError("hipcc link failed:\n" + r.stdout.decode(errors="replace"))
+        os.replace(tmp_lib, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

@@ -1,0 +1,182 @@
+"""ctypes binding of the C ABI in ``include/gdn_recoverssm_hip.h``.
+
+The shared library is built ahead of time into ``_lib/libgdn_recoverssm_hip.so``
+(see ``_build.py``). There is no fallback: if the library is missing or its ABI
+version differs, every launch raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+from ._build import LIB_PATH
+
+ABI_VERSION = 1
+VERIFY_CONFIG_FIELDS = 28
+FOLD_CONFIG_FIELDS = 17
+PLAN_MAX_GROUPS = 8
+
+GDN_OK, GDN_ERR_INVALID, GDN_ERR_UNSUPPORTED, GDN_ERR_LAUNCH = 0, 1, 2, 3
+DT_F32, DT_BF16, DT_F16, DT_I32, DT_I64 = 0, 1, 2, 3, 4
+PLAN_ALIGN, PLAN_PUBLISH, PLAN_GROUPED = 1, 2, 4
+
+_DTYPE_CODES = {
+    torch.float32: DT_F32,
+    torch.bfloat16: DT_BF16,
+    torch.float16: DT_F16,
+    torch.int32: DT_I32,
+    torch.int64: DT_I64,
+}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"GDN RecoverSSM: dtype {dtype} has no HIP kernel") from None
+
+
+c_i64 = ctypes.c_int64
+c_i32 = ctypes.c_int32
+c_vp = ctypes.c_void_p
+P_i64 = ctypes.POINTER(ctypes.c_int64)
+
+
+class VerifyExt(ctypes.Structure):
+    _fields_ = [
+        ("key_dim", c_i64),
+        ("value_dim", c_i64),
+        ("act_dtype", c_i32),
+        ("beta_dtype", c_i32),
+        ("g_dtype", c_i32),
+        ("state_dtype", c_i32),
+        ("key_record_dtype", c_i32),
+        ("qsl_dtype", c_i32),
+        ("index_dtype", c_i32),
+        ("qk_l2norm", c_i32),
+        ("key_per_value_head", c_i32),
+        ("out_dtype", c_i32),
+    ]
+
+
+class FoldExt(ctypes.Structure):
+    _fields_ = [
+        ("key_dim", c_i64),
+        ("value_dim", c_i64),
+        ("state_dtype", c_i32),
+        ("key_dtype", c_i32),
+        ("source_dtype", c_i32),
+        ("reserved", c_i32),
+        ("source_stride", c_i64),
+        ("state_k_stride", c_i64),
+    ]
+
+
+class PlanGroup(ctypes.Structure):
+    _fields_ = [
+        ("state_indices", c_vp), ("si_stride", c_i64), ("si_dtype", c_i32), ("pad0", c_i32),
+        ("query_start_loc", c_vp), ("qsl_stride", c_i64), ("qsl_dtype", c_i32), ("pad1", c_i32),
+        ("request_indices", c_vp), ("map_stride", c_i64), ("map_dtype", c_i32), ("pad2", c_i32),
+        ("block_table", c_vp), ("table_row_stride", c_i64), ("table_col_stride", c_i64), ("table_width", c_i64),
+        ("table_rows", c_i64), ("table_dtype", c_i32), ("pad3", c_i32),
+        ("num_computed", c_vp), ("computed_stride", c_i64), ("computed_len", c_i64), ("computed_dtype", c_i32),
+        ("pad4", c_i32),
+        ("num_blocks", c_i64), ("block_size", c_i64),
+    ]
+
+
+PlanGroups = PlanGroup * PLAN_MAX_GROUPS
+
+_LIB = None
+_LOCK = threading.Lock()
+
+
+def library_path() -> str:
+    return os.environ.get("GDN_RECOVERSSM_HIP_LIB", LIB_PATH)
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once (raises RuntimeError when it is missing)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = library_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"GDN RecoverSSM HIP library not found at {path}; build it with "
+                "`python -m gdn_recoverssm_ascend._build` (there is no fallback path)"
+            )
+        lib = ctypes.CDLL(path)
+        lib.gdn_recoverssm_abi_version.restype = ctypes.c_int
+        lib.gdn_recoverssm_abi_version.argtypes = []
+        lib.gdn_recoverssm_last_error.restype = ctypes.c_char_p
+        lib.gdn_recoverssm_last_error.argtypes = []
+        lib.gdn_recoverssm_verify.restype = ctypes.c_int
+        lib.gdn_recoverssm_verify.argtypes = [c_vp] * 12 + [P_i64, c_i64, ctypes.c_float, ctypes.POINTER(VerifyExt), c_vp]
+        lib.gdn_recoverssm_fold.restype = ctypes.c_int
+        lib.gdn_recoverssm_fold.argtypes = [c_vp] * 18 + [P_i64, c_i64, ctypes.POINTER(FoldExt), c_vp]
+        lib.gdn_recoverssm_plan.restype = ctypes.c_int
+        lib.gdn_recoverssm_plan.argtypes = [
+            c_vp, c_i32, c_i64, c_i64,  # sampled
+            ctypes.POINTER(PlanGroup), c_i32,  # groups
+            c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,  # plan outputs
+            c_vp, c_i32, c_i64,  # idx_mapping
+            c_vp, c_vp, c_i64,  # persistent outputs
+            c_i64, c_i64, c_i64, c_i64, ctypes.c_uint32, c_vp,
+        ]
+        lib.gdn_recoverssm_conv_compact.restype = ctypes.c_int
+        lib.gdn_recoverssm_conv_compact.argtypes = [
+            c_vp, c_vp, c_vp, c_vp,  # tables
+            c_vp, c_i32, c_i64,  # source
+            c_vp, c_vp, c_vp, c_vp, c_vp,  # lengths, final, boundary, boundary_len, layer_groups
+            c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_vp,
+        ]
+        lib.gdn_recoverssm_publish.restype = ctypes.c_int
+        lib.gdn_recoverssm_publish.argtypes = [
+            c_vp, c_i64, c_vp, c_i32, c_i64, c_i64, c_vp, c_i32, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp,
+        ]
+        version = lib.gdn_recoverssm_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"GDN RecoverSSM HIP library ABI mismatch: {version} != {ABI_VERSION}")
+        _LIB = lib
+    return _LIB
+
+
+def exported_symbols() -> tuple[str, ...]:
+    return (
+        "gdn_recoverssm_abi_version",
+        "gdn_recoverssm_last_error",
+        "gdn_recoverssm_verify",
+        "gdn_recoverssm_fold",
+        "gdn_recoverssm_plan",
+        "gdn_recoverssm_conv_compact",
+        "gdn_recoverssm_publish",
+    )
+
+
+def check(status: int, what: str) -> None:
+    if status == GDN_OK:
+        return
+    msg = load().gdn_recoverssm_last_error().decode(errors="replace")
+    if status in (GDN_ERR_INVALID, GDN_ERR_UNSUPPORTED):
+        raise ValueError(f"GDN RecoverSSM: {what} rejected by the HIP library: {msg}")
+    raise RuntimeError(f"GDN RecoverSSM: {what} failed: {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def i64_array(values) -> ctypes.Array:
+    return (c_i64 * len(values))(*[int(v) for v in values])

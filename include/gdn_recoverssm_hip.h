@@ -1,0 +1,177 @@
+/*
+ * gdn_recoverssm_hip.h -- C ABI of the MI355X (gfx950) RecoverSSM kernels.
+ *
+ * Plain pointers, sizes and a hipStream_t (passed as void*); no torch types.
+ * Every entry point validates its arguments on the host and returns a status
+ * code BEFORE anything is launched when they are invalid (the message is kept
+ * in gdn_recoverssm_last_error()). Launches are asynchronous on `stream`, with
+ * no host synchronisation, no allocation and no extra stream, so they can be
+ * captured into a HIP graph.
+ *
+ * Reference interfaces each entry point replaces (paths inside the reference
+ * plugin, plugin/gdn_recoverssm_ascend):
+ *   gdn_recoverssm_abi_version   -> csrc/ops.cpp:244   abi_version() -> 1
+ *   gdn_recoverssm_verify        -> csrc/ops.cpp:87-154, schema :245
+ *                                   (and the Triton launch kernels.py:867-928)
+ *   gdn_recoverssm_fold          -> csrc/ops.cpp:170-239, schema :246
+ *                                   (and grouped_commit.py:837-892, kernels.py:1976-2047)
+ *   gdn_recoverssm_plan          -> grouped_commit.py:741-799 (_grouped_plan_kernel)
+ *                                   and kernels.py:1892-1928 (_prepare_commit_plan_kernel)
+ *   gdn_recoverssm_conv_compact  -> grouped_commit.py:800-836, kernels.py:1931-1973
+ *   gdn_recoverssm_publish       -> grouped_commit.py:531-610 (_publish_grouped_align_kernel)
+ */
+#ifndef GDN_RECOVERSSM_HIP_H
+#define GDN_RECOVERSSM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_RECOVERSSM_ABI_VERSION 1
+
+/* Status codes. */
+#define GDN_OK 0
+#define GDN_ERR_INVALID 1     /* geometry / dtype / stride violation; nothing launched */
+#define GDN_ERR_UNSUPPORTED 2 /* outside what this build implements; nothing launched */
+#define GDN_ERR_LAUNCH 3      /* the HIP runtime rejected the launch */
+
+/* Element type codes for tensors whose dtype is not fixed by the ABI. */
+#define GDN_DT_F32 0
+#define GDN_DT_BF16 1
+#define GDN_DT_F16 2
+#define GDN_DT_I32 3
+#define GDN_DT_I64 4
+
+/* Verify tiling: exactly the 28 integer fields of the reference's
+ * GDN_VERIFY_FIELDS in csrc/common.h:8-36, in that order (strides in elements),
+ * followed by the float scale (csrc/common.h:52-55). */
+#define GDN_VERIFY_CONFIG_FIELDS 28
+/* Fold tiling: the 17 fields of GDN_FOLD_FIELDS, csrc/common.h:37-54. */
+#define GDN_FOLD_CONFIG_FIELDS 17
+
+/* What this build adds over the reference's K=V=128 native specialisation
+ * (csrc/ops.cpp:100-141): dimensions, dtypes and layout flags that the
+ * reference's Triton kernel took as constexprs (kernels.py:534-545). */
+typedef struct gdn_verify_ext {
+  int64_t key_dim;          /* K (<= 256, multiple of 8) */
+  int64_t value_dim;        /* V (>= 1) */
+  int32_t act_dtype;        /* q, k, v, out: F32 / BF16 / F16 */
+  int32_t beta_dtype;       /* activation dtype or F32 */
+  int32_t g_dtype;          /* activation dtype or F32 */
+  int32_t state_dtype;      /* checkpoint: F32 / BF16 / F16 */
+  int32_t key_record_dtype; /* key record: F32 / BF16 / F16 */
+  int32_t qsl_dtype;        /* query_start_loc: I32 / I64 */
+  int32_t index_dtype;      /* state_indices: I32 / I64 */
+  int32_t qk_l2norm;        /* 1: normalise q and k in-kernel (eps 1e-6), kernels.py:645-648 */
+  int32_t key_per_value_head; /* 1: packed record layout, one key per value head, kernels.py:687-697 */
+  int32_t out_dtype;        /* out: F32 / BF16 / F16 (kernels.py:657 stores in out's own dtype) */
+} gdn_verify_ext;
+
+typedef struct gdn_fold_ext {
+  int64_t key_dim;       /* K */
+  int64_t value_dim;     /* V */
+  int32_t state_dtype;   /* F32 / BF16 / F16 */
+  int32_t key_dtype;     /* F32 / BF16 / F16 */
+  int32_t source_dtype;  /* I32 / I64: dtype of `source` */
+  int32_t reserved;
+  int64_t source_stride; /* element stride of `source` (1 for plan arrays; the
+                            table-column stride when the single-context commit
+                            reads state_indices directly, kernels.py:1229) */
+  int64_t state_k_stride;/* must be 1 */
+} gdn_fold_ext;
+
+int gdn_recoverssm_abi_version(void);
+
+/* Last error message of the calling thread ("" when none). */
+const char *gdn_recoverssm_last_error(void);
+
+/* Speculative verify from the read-only checkpoint (kernels.py:491-697).
+ * q, k: [1, T, H, K]; v, out: [1, T, HV, V]; g, beta: [T, HV] (head stride 1);
+ * state: [blocks, HV, V, K] (K stride 1, never written); correction [R, HV, Q, V]
+ * f32; key [R, H, Q, K] (or [R, HV, Q, K]-strided views in packed layout);
+ * decay [R, HV, Q] f32; qsl [rows + 1]; indices [rows] (any element stride). */
+int gdn_recoverssm_verify(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                          const void *state, void *correction, void *key, void *decay, void *out,
+                          const void *qsl, const void *indices, const int64_t *config, int64_t config_len,
+                          float scale, const gdn_verify_ext *ext, void *stream);
+
+/* Grouped fold of the accepted prefix into every layer's checkpoint
+ * (grouped_commit.py:377-480; csrc/fold.h:192-237). All table arguments are
+ * DEVICE pointers: per-layer int64 base addresses / block strides [layers],
+ * int32 layer_groups [layers] (may be NULL: every layer uses group 0), and the
+ * int32 plan arrays [groups * plan_capacity]. state_ref/correction_ref/key_ref/
+ * decay_ref are the first layer's tensors (unused for addressing, as in the
+ * reference, csrc/fold.h:253-273). */
+int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, const void *key_ref, const void *decay_ref,
+                        const int64_t *state_addrs, const int64_t *state_block_strides, const int64_t *corr_addrs,
+                        const int64_t *corr_block_strides, const int64_t *key_addrs,
+                        const int64_t *key_block_strides, const int64_t *decay_addrs,
+                        const int64_t *decay_block_strides, const int32_t *layer_groups, const void *source,
+                        const int32_t *lengths, const int32_t *final_indices, const int32_t *boundary_indices,
+                        const int32_t *boundary_lengths, const int64_t *config, int64_t config_len,
+                        const gdn_fold_ext *ext, void *stream);
+
+/* One cache group of the commit plan (grouped_commit.py:113-146). Pointers are
+ * device pointers; request_indices may be NULL (row i is request i, the
+ * single-context plan of kernels.py:979-983); block_table / num_computed are
+ * NULL in "none" mode. *_len fields bound every index the kernel derives from
+ * data: an index outside them makes the row invalid instead of reading out of
+ * bounds. */
+#define GDN_PLAN_MAX_GROUPS 8
+typedef struct gdn_plan_group {
+  const void *state_indices;   int64_t si_stride;       int32_t si_dtype;       int32_t pad0;
+  const void *query_start_loc; int64_t qsl_stride;      int32_t qsl_dtype;      int32_t pad1;
+  const void *request_indices; int64_t map_stride;      int32_t map_dtype;      int32_t pad2;
+  const void *block_table;     int64_t table_row_stride; int64_t table_col_stride; int64_t table_width;
+  int64_t table_rows;          int32_t table_dtype;     int32_t pad3;
+  const void *num_computed;    int64_t computed_stride; int64_t computed_len;  int32_t computed_dtype; int32_t pad4;
+  int64_t num_blocks;          int64_t block_size;
+} gdn_plan_group;
+
+#define GDN_PLAN_ALIGN 1u     /* align mode: block_table / num_computed present */
+#define GDN_PLAN_PUBLISH 2u   /* publish persistent_cols / persistent_accepted (grouped_commit.py:214-222) */
+#define GDN_PLAN_GROUPED 4u   /* grouped semantics: store the source, canonicalise the boundary
+                                 (grouped_commit.py:194-204); without it the single-context
+                                 semantics of kernels.py:1036-1072 apply */
+
+int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, int64_t sampled_stride, int64_t sampled_len,
+                        const gdn_plan_group *groups, int32_t num_groups, int32_t *source_plan,
+                        int32_t *lens_plan, int32_t *final_plan, int32_t *boundary_plan,
+                        int32_t *boundary_lens_plan, int32_t *valid_plan, int32_t *col_plan,
+                        const void *idx_mapping, int32_t idx_mapping_dtype, int64_t idx_mapping_len,
+                        int32_t *persistent_cols, int32_t *persistent_accepted, int64_t persistent_len,
+                        int64_t num_rows, int64_t plan_capacity, int64_t null_block, int64_t spec_query_len,
+                        uint32_t flags, void *stream);
+
+/* Conv-state compaction (grouped_commit.py:225-322 / kernels.py:1075-1169).
+ * Per-layer DEVICE tables: base addresses, block / dim / token strides
+ * (elements). element_bytes is 2 or 4. `source` as in gdn_recoverssm_fold.
+ * history is the kept history length, window the conv state's token extent
+ * (history + Q - 1); every token read stays inside the window. */
+int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int64_t *conv_block_strides,
+                                const int64_t *conv_dim_strides, const int64_t *conv_token_strides,
+                                const void *source, int32_t source_dtype, int64_t source_stride,
+                                const int32_t *lengths, const int32_t *final_indices,
+                                const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                                const int32_t *layer_groups, int64_t plan_capacity, int64_t null_block,
+                                int64_t num_rows, int64_t num_layers, int64_t conv_dim, int64_t history,
+                                int64_t window, int64_t num_blocks, int32_t element_bytes, int32_t align,
+                                void *stream);
+
+/* AND-valid publication across buckets (grouped_commit.py:531-560).
+ * descriptors: DEVICE int64 [num_buckets * 4] = (valid ptr, col ptr, capacity,
+ * group count) per bucket. request_len is the number of entries of
+ * request_indices (at least num_rows). */
+int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_buckets, const void *request_indices,
+                           int32_t request_dtype, int64_t request_stride, int64_t request_len,
+                           const void *idx_mapping, int32_t idx_mapping_dtype, int64_t idx_mapping_len,
+                           int32_t *persistent_cols, int32_t *persistent_accepted, int64_t persistent_len,
+                           int64_t num_rows, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_RECOVERSSM_HIP_H */

@@ -1,0 +1,122 @@
+"""The C-ABI library: builds, loads without a GPU, exports every declared
+symbol, and its ctypes struct layouts match what the C compiler lays out.
+No compute entry point is called with real work here (no GPU on this host)."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from gdn_recoverssm_ascend import _native as N
+from gdn_recoverssm_ascend._build import INCLUDE_DIR, LIB_PATH
+
+HEADER = os.path.join(INCLUDE_DIR, "gdn_recoverssm_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(gdn_recoverssm_\w+)\s*\(", text)))
+
+
+def test_library_is_built():
+    assert os.path.exists(LIB_PATH), "run `python -c 'import __graft_entry__ as g; g.build()'` first"
+
+
+def test_every_declared_symbol_is_exported():
+    lib = ctypes.CDLL(LIB_PATH)
+    declared = _declared_symbols()
+    assert set(declared) == set(N.exported_symbols())
+    for name in declared:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True).stdout
+    for name in declared:
+        assert re.search(rf"\bT {name}\b", out), f"{name} not exported with C linkage"
+
+
+def test_abi_version_and_error_channel():
+    lib = N.load()
+    assert lib.gdn_recoverssm_abi_version() == N.ABI_VERSION == 1
+    assert isinstance(lib.gdn_recoverssm_last_error(), bytes)
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = N.load()
+    ext = N.VerifyExt(key_dim=128, value_dim=128)
+    cfg = N.i64_array([0] * 27)
+    st = lib.gdn_recoverssm_verify(*([None] * 12), cfg, 27, 1.0, ctypes.byref(ext), None)
+    assert st == N.GDN_ERR_INVALID
+    assert b"28 config fields" in lib.gdn_recoverssm_last_error()
+    # geometry: value heads not a multiple of key heads
+    cfg = N.i64_array([1, 4, 3, 4, 4, 8, 1, 0] + [0] * 20)
+    st = lib.gdn_recoverssm_verify(*([None] * 12), cfg, 28, 1.0, ctypes.byref(ext), None)
+    assert st == N.GDN_ERR_INVALID and b"geometry" in lib.gdn_recoverssm_last_error()
+    # unsupported key dim
+    ext2 = N.VerifyExt(key_dim=512, value_dim=128)
+    cfg = N.i64_array([1, 4, 1, 2, 4, 8, 1, 0] + [0] * 20)
+    st = lib.gdn_recoverssm_verify(*([None] * 12), cfg, 28, 1.0, ctypes.byref(ext2), None)
+    assert st == N.GDN_ERR_UNSUPPORTED
+    # fold with the wrong field count
+    fext = N.FoldExt(key_dim=128, value_dim=128)
+    st = lib.gdn_recoverssm_fold(*([None] * 18), N.i64_array([0] * 16), 16, ctypes.byref(fext), None)
+    assert st == N.GDN_ERR_INVALID
+    # plan with no groups, conv with a bad element size, publish without outputs
+    groups = N.PlanGroups()
+    st = lib.gdn_recoverssm_plan(None, 3, 1, 0, groups, 0, *([None] * 7), None, 3, 0, None, None, 0, 1, 1, 0, 4, 0, None)
+    assert st == N.GDN_ERR_INVALID
+    st = lib.gdn_recoverssm_publish(None, 1, None, 3, 1, 1, None, 3, 1, None, None, 1, 1, None)
+    assert st == N.GDN_ERR_INVALID
+
+
+def test_zero_rows_is_a_noop_without_touching_the_device():
+    lib = N.load()
+    ext = N.VerifyExt(key_dim=128, value_dim=128, act_dtype=1, out_dtype=1, state_dtype=0, key_record_dtype=1,
+                      qsl_dtype=3, index_dtype=3)
+    cfg = N.i64_array([0, 0, 1, 2, 4, 8, 1, 0] + [0] * 20)
+    assert lib.gdn_recoverssm_verify(*([None] * 12), cfg, 28, 1.0, ctypes.byref(ext), None) == N.GDN_OK
+
+
+_LAYOUT_PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "gdn_recoverssm_hip.h"
+#define F(T, f) printf("%s.%s %zu\n", #T, #f, offsetof(T, f));
+int main(void) {
+  printf("gdn_verify_ext %zu\n", sizeof(gdn_verify_ext));
+  printf("gdn_fold_ext %zu\n", sizeof(gdn_fold_ext));
+  printf("gdn_plan_group %zu\n", sizeof(gdn_plan_group));
+  F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
+  F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride)
+  F(gdn_plan_group, block_table) F(gdn_plan_group, table_rows) F(gdn_plan_group, num_computed)
+  F(gdn_plan_group, computed_dtype) F(gdn_plan_group, num_blocks) F(gdn_plan_group, block_size)
+  return 0;
+}
+"""
+
+
+def test_ctypes_struct_layout_matches_c_compiler():
+    with tempfile.TemporaryDirectory() as tmp:
+        src = os.path.join(tmp, "probe.c")
+        exe = os.path.join(tmp, "probe")
+        open(src, "w").write(_LAYOUT_PROBE)
+        subprocess.run(["gcc", "-I", INCLUDE_DIR, src, "-o", exe], check=True)
+        lines = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = dict(line.rsplit(" ", 1) for line in lines if line)
+    assert int(got["gdn_verify_ext"]) == ctypes.sizeof(N.VerifyExt)
+    assert int(got["gdn_fold_ext"]) == ctypes.sizeof(N.FoldExt)
+    assert int(got["gdn_plan_group"]) == ctypes.sizeof(N.PlanGroup)
+    for key, value in got.items():
+        if "." not in key:
+            continue
+        struct, fld = key.split(".")
+        cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup}[struct]
+        assert getattr(cls, fld).offset == int(value), key
+
+
+def test_config_field_counts_match_reference_abi():
+    # csrc/common.h of the reference: 28 verify fields (+ scale), 17 fold fields
+    text = open(HEADER).read()
+    assert "#define GDN_VERIFY_CONFIG_FIELDS 28" in text and N.VERIFY_CONFIG_FIELDS == 28
+    assert "#define GDN_FOLD_CONFIG_FIELDS 17" in text and N.FOLD_CONFIG_FIELDS == 17

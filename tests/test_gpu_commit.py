@@ -1,0 +1,307 @@
+"""GPU parity of the commit path (plan, conv compaction, fold, publication).
+
+Bar: plan arrays, conv histories and persistent publication bit-exact; FP32
+committed state within max-abs 1e-5 of the oracle relative to the pages'
+max-abs; pages the commit does not target bit-identical.
+"""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+import gdn_oracle as O
+from gdn_recoverssm_ascend.grouped_commit import CommitEntry, GroupedCommitBucket, GroupedCommitCoordinator
+from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers
+from gpu_helpers import assert_state_close
+
+pytestmark = pytest.mark.gpu
+
+CONV_DIM = 40
+HIST = 3
+
+
+@pytest.fixture(scope="module")
+def dev(gpu_device):
+    return gpu_device
+
+
+def _l2(x):
+    return x * torch.rsqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+
+def _group(B, H, HV, K, V, Q, L, *, align, seed, Bk=8, key_dtype=torch.bfloat16, state_dtype=torch.float32,
+           packed=False, accepted=None, page_offset=0, qlens=None):
+    """One cache group: L layers of pages, records and per-step metadata (CPU)."""
+    gen = torch.Generator().manual_seed(seed)
+    acc = torch.randint(0, Q + 1, (B,), generator=gen, dtype=torch.int32) if accepted is None else accepted.clone()
+    qlens = torch.full((B,), Q) if qlens is None else torch.tensor(qlens)
+    qsl = torch.zeros(B + 1, dtype=torch.int32)
+    qsl[1:] = torch.cumsum(qlens, 0)
+    if align:
+        C = torch.randint(0, 5 * Bk, (B,), generator=gen)
+        for r in range(0, B, 2):  # half the rows cross a boundary inside the window
+            n = int(acc[r])
+            if n >= 1:
+                ahead = int(torch.randint(1, n + 1, (1,), generator=gen))
+                C[r] = max(int(C[r]) // Bk, 1) * Bk - ahead
+        W = 5 + 3
+        table = torch.zeros(B, W, dtype=torch.int32)
+        src_col = torch.clamp(C - 1, min=0) // Bk
+        for r in range(B):
+            for j in range(3):
+                table[r, int(src_col[r]) + j] = 1 + page_offset + 3 * r + j
+        NB = 1 + page_offset + 3 * B + 2
+        src = table[torch.arange(B), src_col].clone()
+        num_computed = C.to(torch.int32)
+    else:
+        NB = 1 + page_offset + B + 3
+        src = (torch.randperm(B + 3, generator=gen)[:B] + 1 + page_offset).to(torch.int32)
+        table = num_computed = None
+    ckpts, convs, recs = [], [], []
+    for _ in range(L):
+        ckpts.append((torch.randn(NB, HV, V, K, generator=gen) * 0.1).to(state_dtype))
+        convs.append(torch.randn(NB, CONV_DIM, HIST + Q - 1, generator=gen).to(torch.bfloat16))
+        corr = torch.randn(B, HV, Q, V, generator=gen)
+        key = _l2(torch.randn(B, H, Q, K, generator=gen)).to(key_dtype)
+        decay = torch.rand(B, HV, Q, generator=gen) * 0.5 + 0.5
+        if packed:
+            keyv = key.float().repeat_interleave(HV // H, dim=1)
+            recs.append(torch.cat([corr, keyv, decay[..., None]], dim=-1))
+        else:
+            recs.append((corr, key, decay))
+    return dict(B=B, H=H, HV=HV, K=K, V=V, Q=Q, L=L, NB=NB, acc=acc, qsl=qsl, src=src, table=table,
+                C=num_computed, Bk=Bk if align else None, ckpts=ckpts, convs=convs, recs=recs, packed=packed)
+
+
+def _to_dev(G, dev):
+    ckpts = [c.to(dev) for c in G["ckpts"]]
+    convs = [c.to(dev) for c in G["convs"]]
+    if G["packed"]:
+        recs = [r.to(dev) for r in G["recs"]]
+    else:
+        recs = [ReplayRecordBuffers(*(t.to(dev) for t in r)) for r in G["recs"]]
+    return ckpts, convs, recs
+
+
+def _planes(G):
+    if G["packed"]:
+        V, K = G["V"], G["K"]
+        return ([r[..., :V] for r in G["recs"]], [r[..., V:V + K] for r in G["recs"]], [r[..., V + K] for r in G["recs"]])
+    return tuple([r[i] for r in G["recs"]] for i in range(3))
+
+
+def _check_states(got_list, want_list, state_dtype, targeted_pages):
+    for li, (got, want) in enumerate(zip(got_list, want_list)):
+        got = got.cpu()
+        untouched = [p for p in range(got.shape[0]) if p not in targeted_pages]
+        assert torch.equal(got[untouched], want[untouched]), f"layer {li}: untouched pages changed"
+        if state_dtype == torch.float32:
+            assert_state_close(got, want, f"layer {li} state")
+        else:
+            err = O.max_abs_rel(got, want)
+            assert err <= 8e-3, f"layer {li}: {err}"
+
+
+@pytest.mark.parametrize("align", [False, True])
+@pytest.mark.parametrize("packed", [False, True])
+def test_single_context_commit(dev, align, packed):
+    G = _group(12, 2, 4, 128, 128, 4, 2, align=align, seed=3 + align + 2 * packed, packed=packed)
+    ckpts, convs, recs = _to_dev(G, dev)
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=16)
+    ctx.commit(
+        G["acc"].to(dev), G["src"].to(dev), G["qsl"].to(dev),
+        block_table=None if not align else G["table"].to(dev),
+        num_computed_tokens=None if not align else G["C"].to(dev),
+        mamba_block_size=G["Bk"],
+    )
+    torch.cuda.synchronize()
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=4, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    B = G["B"]
+    assert ctx.commit_lens[:B].cpu().tolist() == plan["commit_lens"].tolist()
+    assert ctx.final_state_indices[:B].cpu().tolist() == plan["final"].tolist()
+    assert ctx.boundary_state_indices[:B].cpu().tolist() == plan["boundary"].tolist()
+    assert ctx.boundary_recovery_lens[:B].cpu().tolist() == plan["boundary_len"].tolist()
+    assert ctx.align_valid[:B].cpu().tolist() == plan["align_valid"].tolist()
+    assert ctx.align_col[:B].cpu().tolist() == plan["align_col"].tolist()
+    corrs, keys, decays = _planes(G)
+    want = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=G["src"], lengths=plan["commit_lens"],
+                         final=plan["final"], boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                         rows=B, num_blocks=G["NB"], record_rows=B)
+    targeted = set(plan["final"].tolist()) | set(plan["boundary"].tolist())
+    _check_states(ckpts, want, torch.float32, targeted)
+    want_conv = O.oracle_conv_compact(G["convs"], source=G["src"], lengths=plan["commit_lens"], final=plan["final"],
+                                      boundary=plan["boundary"], boundary_len=plan["boundary_len"], history=HIST,
+                                      num_blocks=G["NB"], rows=B, align=align)
+    for got, w in zip(convs, want_conv):
+        assert torch.equal(got.cpu(), w)
+    if align:
+        assert int(plan["boundary_len"].gt(0).sum()) > 0, "the case must exercise boundary snapshots"
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 3, 4])
+def test_commit_every_accepted_length(dev, n):
+    B = 6
+    G = _group(B, 2, 4, 128, 128, 4, 1, align=True, seed=20 + n, accepted=torch.full((B,), n, dtype=torch.int32))
+    ckpts, convs, recs = _to_dev(G, dev)
+    before = [c.clone() for c in ckpts]
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+    ctx.commit(G["acc"].to(dev), G["src"].to(dev), G["qsl"].to(dev), block_table=G["table"].to(dev),
+               num_computed_tokens=G["C"].to(dev), mamba_block_size=G["Bk"], commit_conv=False)
+    torch.cuda.synchronize()
+    if n == 0:
+        assert all(torch.equal(a, b) for a, b in zip(ckpts, before)), "n = 0 must leave every page bit-identical"
+        return
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=4, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    corrs, keys, decays = _planes(G)
+    want = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=G["src"], lengths=plan["commit_lens"],
+                         final=plan["final"], boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                         rows=B, num_blocks=G["NB"], record_rows=B)
+    _check_states(ckpts, want, torch.float32, set(plan["final"].tolist()) | set(plan["boundary"].tolist()))
+
+
+@pytest.mark.parametrize("state_dtype,key_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                                   (torch.float16, torch.float16)])
+def test_commit_dtypes(dev, state_dtype, key_dtype):
+    G = _group(8, 2, 4, 128, 128, 4, 1, align=True, seed=41, key_dtype=key_dtype, state_dtype=state_dtype)
+    ckpts, convs, recs = _to_dev(G, dev)
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=8)
+    ctx.commit(G["acc"].to(dev), G["src"].to(dev), G["qsl"].to(dev), block_table=G["table"].to(dev),
+               num_computed_tokens=G["C"].to(dev), mamba_block_size=G["Bk"])
+    torch.cuda.synchronize()
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=4, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    corrs, keys, decays = _planes(G)
+    want = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=G["src"], lengths=plan["commit_lens"],
+                         final=plan["final"], boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                         rows=8, num_blocks=G["NB"], record_rows=8)
+    _check_states(ckpts, want, state_dtype, set(plan["final"].tolist()) | set(plan["boundary"].tolist()))
+
+
+def _entry(G, ctx, dev, request_rows):
+    table = torch.zeros(G["B"], G["Q"], dtype=torch.int32, device=dev)
+    table[:, 0] = G["src"].to(dev)
+    payload = SimpleNamespace(
+        state_indices=table[:, 0],
+        query_start_loc=G["qsl"].to(dev),
+        request_indices=torch.tensor(request_rows, dtype=torch.int64, device=dev),
+        block_table=None if G["table"] is None else G["table"].to(dev),
+        num_computed_tokens=None if G["C"] is None else G["C"].to(dev),
+        block_size=G["Bk"],
+        request_rows=tuple(request_rows),
+        query_lens=tuple(int(G["qsl"][i + 1] - G["qsl"][i]) for i in range(G["B"])),
+    )
+    meta = SimpleNamespace(recoverssm_commit=payload, recoverssm_builder=SimpleNamespace(), recoverssm_context=ctx)
+    return CommitEntry(meta, payload, ctx)
+
+
+def _oracle_grouped(groups, sampled, mapping, cols, acc, request_rows, align, capacity, publish=True):
+    og = []
+    for G in groups:
+        og.append(dict(state_indices=G["src"], query_start_loc=G["qsl"], request_indices=torch.tensor(request_rows),
+                       block_table=G["table"], num_computed=G["C"], block_size=G["Bk"], num_blocks=G["NB"]))
+    return O.oracle_plan_grouped(sampled, og, spec_query_len=groups[0]["Q"], capacity=capacity, rows=groups[0]["B"],
+                                 align=align, idx_mapping=mapping, persistent_cols=cols, persistent_accepted=acc,
+                                 publish_align=publish)
+
+
+@pytest.mark.parametrize("align", [True, False])
+def test_grouped_bucket_two_groups_reordered_rows(dev, align):
+    B = 6
+    request_rows = [2, 0, 5, 1, 4, 3]
+    sampled = torch.tensor([4, 0, 3, 1, 2, 4], dtype=torch.int32)
+    groups = [_group(B, 2, 4, 128, 128, 4, 2, align=align, seed=60 + g, page_offset=10 * g) for g in range(2)]
+    # the accepted count is indexed by request; share it between groups
+    contexts, entries, devs = [], [], []
+    for G in groups:
+        ckpts, convs, recs = _to_dev(G, dev)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+        contexts.append(ctx)
+        devs.append((ckpts, convs))
+        entries.append(_entry(G, ctx, dev, request_rows))
+    bucket = GroupedCommitBucket(tuple(contexts))
+    mapping = torch.tensor([3, 1, -1, 0, 5, 2], dtype=torch.int32)
+    cols = torch.full((7,), -9, dtype=torch.int32)
+    accp = torch.full((7,), 7, dtype=torch.int32)
+    cols_d, accp_d = cols.to(dev), accp.to(dev)
+    specs = bucket.make_specs(entries, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
+    assert [s.name for s in specs] == ["plan", "conv", "fold"]
+    for s in specs:
+        s.launch()
+    torch.cuda.synchronize()
+    want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, align, bucket.capacity)
+    cap = bucket.capacity
+    for name, arr in (("source", bucket.source), ("length", bucket.length), ("final", bucket.final),
+                      ("boundary", bucket.boundary), ("boundary_len", bucket.boundary_len), ("valid", bucket.valid),
+                      ("col", bucket.col)):
+        got = arr.cpu()
+        for gi in range(2):
+            seg = slice(gi * cap, gi * cap + B)
+            assert got[seg].tolist() == want[name][seg].tolist(), (name, gi)
+    if align:
+        assert cols_d.cpu().tolist() == want["persistent_cols"].tolist()
+        assert accp_d.cpu().tolist() == want["persistent_accepted"].tolist()
+    else:
+        assert accp_d.cpu().tolist() == [7] * 7
+    for gi, G in enumerate(groups):
+        seg = slice(gi * cap, gi * cap + cap)
+        corrs, keys, decays = _planes(G)
+        wstate = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=want["source"][seg], lengths=want["length"][seg],
+                               final=want["final"][seg], boundary=want["boundary"][seg],
+                               boundary_len=want["boundary_len"][seg], rows=B, num_blocks=G["NB"], record_rows=B)
+        targeted = set(want["final"][seg].tolist()) | set(want["boundary"][seg].tolist())
+        _check_states(devs[gi][0], wstate, torch.float32, targeted)
+        wconv = O.oracle_conv_compact(G["convs"], source=want["source"][seg], lengths=want["length"][seg],
+                                      final=want["final"][seg], boundary=want["boundary"][seg],
+                                      boundary_len=want["boundary_len"][seg], history=HIST, num_blocks=G["NB"],
+                                      rows=B, align=align)
+        for got, w in zip(devs[gi][1], wconv):
+            assert torch.equal(got.cpu(), w)
+
+
+def test_coordinator_seven_groups_three_buckets_and_publication(dev):
+    B = 4
+    request_rows = [1, 3, 0, 2]
+    sampled = torch.tensor([2, 4, 0, 3], dtype=torch.int32)
+    groups = [_group(B, 2, 4, 64, 64, 4, 1, align=True, seed=80 + g) for g in range(7)]
+    # All groups share the same logical rows, positions and block size.
+    for G in groups[1:]:
+        G["C"] = groups[0]["C"].clone()
+        G["qsl"] = groups[0]["qsl"].clone()
+    metas, devs, contexts = [], [], []
+    for G in groups:
+        # re-derive the table/source from the shared positions
+        C = G["C"].long()
+        src_col = torch.clamp(C - 1, min=0) // G["Bk"]
+        table = torch.zeros_like(G["table"])
+        for r in range(B):
+            for j in range(3):
+                table[r, int(src_col[r]) + j] = 1 + 3 * r + j
+        G["table"], G["src"] = table, table[torch.arange(B), src_col].clone()
+        ckpts, convs, recs = _to_dev(G, dev)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+        contexts.append(ctx)
+        devs.append((ckpts, convs))
+        metas.append(_entry(G, ctx, dev, request_rows).metadata)
+    mapping = torch.tensor([2, -1, 0, 3], dtype=torch.int32)
+    cols = torch.full((5,), -9, dtype=torch.int32)
+    accp = torch.full((5,), 7, dtype=torch.int32)
+    cols_d, accp_d = cols.to(dev), accp.to(dev)
+    coord = GroupedCommitCoordinator()
+    coord.commit(metas, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
+    torch.cuda.synchronize()
+    assert coord.last_group_count == 7 and coord.last_launch_count == 10
+    assert [len(b.contexts) for b in coord._buckets.values()] == [3, 3, 1]
+    want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, True, B)
+    assert cols_d.cpu().tolist() == want["persistent_cols"].tolist()
+    assert accp_d.cpu().tolist() == want["persistent_accepted"].tolist()
+    for gi, G in enumerate(groups):
+        seg = slice(gi * B, gi * B + B)
+        corrs, keys, decays = _planes(G)
+        wstate = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=want["source"][seg], lengths=want["length"][seg],
+                               final=want["final"][seg], boundary=want["boundary"][seg],
+                               boundary_len=want["boundary_len"][seg], rows=B, num_blocks=G["NB"], record_rows=B)
+        targeted = set(want["final"][seg].tolist()) | set(want["boundary"][seg].tolist())
+        _check_states(devs[gi][0], wstate, torch.float32, targeted)
