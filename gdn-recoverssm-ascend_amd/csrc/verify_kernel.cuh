@@ -1,0 +1,429 @@
+// Speculative verify of a Gated DeltaNet window from the read-only checkpoint
+// (kernels.py:491-697 and csrc/verify.h:284-332 of the reference plugin).
+//
+// Per (row b, value head hv) the reference advances S <- S*d_t + c_t k_t^T
+// token by token. Verify never writes the state back, so this kernel never
+// forms S_t: with G_t = d_0 ... d_t,
+//     S_{t-1} k_t = G_{t-1} S_0 k_t + sum_{s<t} (G_{t-1}/G_s) (k_s.k_t) c_s
+//     S_t q~_t    = G_t     S_0 q~_t + sum_{s<=t} (G_t/G_s)   (k_s.q~_t) c_s
+// The state enters only through the 2Q matrix-vector products
+// S_0 [k_0 .. k_{Q-1}, q~_0 .. q~_{Q-1}], computed on the matrix cores
+// (v_mfma_f32_16x16x4_f32, FP32 in and out) from one read of the state; the
+// per-row recurrence then runs on Q-vectors with the Gram matrix
+// k_s.{k_t, q~_t}, evaluated incrementally (no divisions):
+//     u_j <- d_t u_j + c_t (k_t.k_j),  w_j <- d_t w_j + c_t (k_t.q~_j).
+//
+// Work decomposition: one wave per (row, value head, 128-row tile of V). The
+// tile is eight 16-row MFMA blocks streamed through two register buffers: the
+// loads of blocks i+2 and i+3 are in flight while blocks i and i+1 are on the
+// matrix cores, and each 64-row half runs its recurrence while the next
+// half's loads are outstanding. Everything the recurrence needs from memory
+// (v, gates) is loaded before the first state block, because the vector memory
+// counter retires in issue order.
+//
+// MFMA operand layout (16x16x4, wave64): A lane l = (row l%16, k-slot l/16),
+// B lane l = (k-slot l/16, column l%16), D lane l register r = (row
+// 4*(l/16)+r, column l%16). Lane (i, s) loads the 16-byte chunks 4j+s of its
+// row, so the k-slot s of MFMA (j, e) holds element E*(4j+s)+e; B uses the
+// same permutation of K.
+//
+// Template parameters: S state element type, A activation type (q, k, v and
+// the key record / output when they share it), J 16-byte chunks per lane per
+// row (K <= 4*E*J), QM window capacity (Q <= QM).
+#pragma once
+
+#include "gdn_common.cuh"
+
+namespace gdn {
+
+struct VerifyArgs {
+  const void *q, *k, *v, *g, *beta;
+  const void *state;
+  float *corr;
+  void *key;
+  float *decay;
+  void *out;
+  const void *qsl, *indices;
+  int64_t state_bs, q_ts, k_ts, v_ts, g_ts, beta_ts;
+  int64_t corr_rs, key_rs, decay_rs, out_ts;
+  int64_t qsl_s, idx_s;
+  int64_t blocks, null_block;
+  int32_t tokens, heads, value_heads, Q, record_rows;
+  int32_t state_hs, state_vs;
+  int32_t corr_hs, corr_ts, key_hs, key_ts, decay_hs, decay_ts;
+  float scale;
+  int32_t K, V, NVT;
+  int32_t qsl_i64, idx_i64;                  // index dtypes: 1 for int64
+  int32_t g_f32, beta_f32, key_f32, out_f32;  // 1: FP32, 0: activation dtype
+  int32_t l2norm, key_per_value_head, vec4;
+};
+
+constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
+constexpr int kTileRows = 128;     // eight MFMA row blocks of 16 rows
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename A>
+__device__ __forceinline__ float ld_act(const void *p, int64_t i) {
+  return to_f32(static_cast<const A *>(p)[i]);
+}
+
+// f32 or activation-typed scalar, chosen by a wave-uniform flag.
+template <typename A>
+__device__ __forceinline__ float ld_f32_or(const void *p, int64_t i, bool f32) {
+  return f32 ? static_cast<const float *>(p)[i] : ld_act<A>(p, i);
+}
+
+template <typename A>
+__device__ __forceinline__ void st_f32_or(void *p, int64_t i, bool f32, float x) {
+  if (f32)
+    static_cast<float *>(p)[i] = x;
+  else
+    static_cast<A *>(p)[i] = from_f32<A>(x);
+}
+
+// Four consecutive activation elements (one 8- or 16-byte load when aligned).
+template <typename A>
+__device__ __forceinline__ void ld4_act(const void *p, int64_t off, bool vec, float *x) {
+  if constexpr (sizeof(A) == 4) {
+    if (vec) {
+      const float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + off);
+      x[0] = f.x, x[1] = f.y, x[2] = f.z, x[3] = f.w;
+      return;
+    }
+  } else {
+    if (vec) {
+      const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const A *>(p) + off);
+      x[0] = to_f32(__builtin_bit_cast(A, uint16_t(u.x & 0xffffu)));
+      x[1] = to_f32(__builtin_bit_cast(A, uint16_t(u.x >> 16)));
+      x[2] = to_f32(__builtin_bit_cast(A, uint16_t(u.y & 0xffffu)));
+      x[3] = to_f32(__builtin_bit_cast(A, uint16_t(u.y >> 16)));
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = ld_act<A>(p, off + i);
+}
+
+template <typename S>
+__device__ __forceinline__ float chunk_elem(const uint4 &raw, int e);
+template <>
+__device__ __forceinline__ float chunk_elem<float>(const uint4 &raw, int e) {
+  return __uint_as_float(e == 0 ? raw.x : e == 1 ? raw.y : e == 2 ? raw.z : raw.w);
+}
+template <>
+__device__ __forceinline__ float chunk_elem<bf16>(const uint4 &raw, int e) {
+  const uint32_t w = (e >> 1) == 0 ? raw.x : (e >> 1) == 1 ? raw.y : (e >> 1) == 2 ? raw.z : raw.w;
+  return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+template <>
+__device__ __forceinline__ float chunk_elem<f16>(const uint4 &raw, int e) {
+  const uint32_t w = (e >> 1) == 0 ? raw.x : (e >> 1) == 1 ? raw.y : (e >> 1) == 2 ? raw.z : raw.w;
+  return float(__builtin_bit_cast(f16, uint16_t((e & 1) ? (w >> 16) : (w & 0xffffu))));
+}
+
+__device__ __forceinline__ int64_t ld_idx(const void *p, int64_t i, bool i64) {
+  return i64 ? static_cast<const int64_t *>(p)[i] : int64_t(static_cast<const int32_t *>(p)[i]);
+}
+
+template <typename S, typename A, int J, int QM>
+__global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
+  constexpr int E = Chunk<S>::E;       // elements per 16-byte chunk
+  constexpr int KP = 4 * E * J;        // K padded to 4 k-slots x J chunks x E
+  constexpr int NV = 2 * QM;           // used MFMA columns (<= 16)
+  constexpr int MP = KP + 4;           // LDS row pitch of the k/q vectors (bank spread)
+  constexpr int NRB = kTileRows / 16;  // 16-row MFMA blocks per tile
+  __shared__ float m_lds[NV][MP];
+  __shared__ float gram_lds[QM][NV];
+  __shared__ float d_lds[64][NV + 1];  // GEMV results of one 64-row half tile
+  __shared__ float inv_lds[NV];
+
+  const int nvt = a.NVT;
+  const int hv = int(blockIdx.x) / nvt;
+  const int vt = int(blockIdx.x) - hv * nvt;
+  const int b = int(blockIdx.y);
+  const int ratio = a.value_heads / a.heads;
+  const int h = hv / ratio;
+  const int lane = threadIdx.x;
+  const int V = a.V, K = a.K;
+  const int row0 = vt * kTileRows;
+  const int Q = a.Q;
+
+  const int64_t bos = ld_idx(a.qsl, int64_t(b) * a.qsl_s, a.qsl_i64);
+  const int64_t eos = ld_idx(a.qsl, int64_t(b + 1) * a.qsl_s, a.qsl_i64);
+  const int64_t qlen = eos - bos;
+  const int64_t slot = ld_idx(a.indices, int64_t(b) * a.idx_s, a.idx_i64);
+  const int64_t out_base = int64_t(hv) * V + row0;
+
+  if (slot <= a.null_block || slot >= a.blocks) {
+    // Null or out-of-range page: zero outputs for the window, records untouched
+    // (kernels.py:569-583).
+    for (int t = 0; t < Q; ++t) {
+      const int64_t tok = bos + t;
+      if (!(t < qlen && tok >= 0 && tok < a.tokens)) continue;
+      for (int r = lane; r < kTileRows; r += kVerifyThreads)
+        if (row0 + r < V) st_f32_or<A>(a.out, tok * a.out_ts + out_base + r, a.out_f32 != 0, 0.0f);
+    }
+    return;
+  }
+  // Token validity is uniform across the wave (kernels.py:612).
+  uint32_t valid_mask = 0;
+#pragma unroll
+  for (int t = 0; t < QM; ++t) {
+    const int64_t tok = bos + t;
+    if (t < Q && t < qlen && tok >= 0 && tok < a.tokens) valid_mask |= 1u << t;
+  }
+  if (valid_mask == 0) return;
+
+  const int li = lane & 15, ls = lane >> 4;  // MFMA row / column index and k-slot
+
+  // ---- 1. small loads first: k/q chunks, gates, v of the lane's rows ----
+  constexpr int C4 = KP / 4;  // 4-element chunks per vector
+  constexpr int STAGE_PASSES = (NV * C4 + kVerifyThreads - 1) / kVerifyThreads;
+  float xs[STAGE_PASSES][4];
+#pragma unroll
+  for (int p = 0; p < STAGE_PASSES; ++p) {
+    const int idx = p * kVerifyThreads + lane;
+    const int vid = idx / C4, kk = (idx - vid * C4) * 4;
+    const bool is_q = vid >= QM;
+    const int t = is_q ? vid - QM : vid;
+    const bool live = vid < NV && ((valid_mask >> t) & 1u) && kk < K;
+    if (live) {
+      const int64_t off = (bos + t) * (is_q ? a.q_ts : a.k_ts) + int64_t(h) * K + kk;
+      ld4_act<A>(is_q ? a.q : a.k, off, a.vec4 != 0, xs[p]);
+    } else {
+      xs[p][0] = xs[p][1] = xs[p][2] = xs[p][3] = 0.0f;
+    }
+  }
+  // Gates are wave-uniform: keep them in scalar registers.
+  float dec[QM], bet[QM];
+#pragma unroll
+  for (int t = 0; t < QM; ++t) {
+    const bool tv = (valid_mask >> t) & 1u;
+    const int64_t tok = bos + t;
+    const float d = tv ? expf(ld_f32_or<A>(a.g, tok * a.g_ts + hv, a.g_f32 != 0)) : 1.0f;
+    const float be = tv ? ld_f32_or<A>(a.beta, tok * a.beta_ts + hv, a.beta_f32 != 0) : 0.0f;
+    dec[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(d)));
+    bet[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(be)));
+  }
+  // v of the lane's row in each half; the second half is loaded later, after
+  // the loads it must not wait behind.
+  float vv[2][QM];
+  auto load_v = [&](int half) {
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const int vr = row0 + half * 64 + lane;
+      vv[half][t] = (vr < V && ((valid_mask >> t) & 1u))
+                        ? ld_act<A>(a.v, (bos + t) * a.v_ts + out_base + half * 64 + lane)
+                        : 0.0f;
+    }
+  };
+  load_v(0);
+
+  // ---- 2. first two state blocks ----
+  // Buffer loads: one resource per (slot, head) tile, a 32-bit per-lane offset,
+  // the block step in soffset and the chunk step in the immediate. Rows >= V
+  // lie past the resource's extent and read as zero; so do chunks >= K.
+  // Rows of block rb: rb*16 + li; the lane loads chunks 4j + ls of its row.
+  const S *sp = static_cast<const S *>(a.state) + slot * a.state_bs + int64_t(hv) * a.state_hs +
+                int64_t(row0) * a.state_vs;
+  const int tile_rows = V - row0 < kTileRows ? V - row0 : kTileRows;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<S *>(sp), 0, tile_rows * a.state_vs * int(sizeof(S)), 0x00020000);
+  const int row_bytes = a.state_vs * int(sizeof(S));
+  const int lane_off = li * row_bytes + ls * 16;
+  const bool full_k = K == KP;  // no chunk past K: plain offsets, chunk step in the immediate
+  auto load_block = [&](int rb, uint4 (&dst)[J]) {
+    if (full_k) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        dst[j] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off + j * 64, rb * 16 * row_bytes, 0));
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : 0x7ffff000;
+        dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
+      }
+    }
+  };
+  uint4 bufA[J], bufB[J];
+  load_block(0, bufA);
+  load_block(1, bufB);
+
+  // ---- 3. stage vectors and records ----
+  const bool rec_ok = b < a.record_rows;
+  const bool key_writer = rec_ok && vt == 0 && (a.key_per_value_head || (hv % ratio) == 0);
+  const int key_head = a.key_per_value_head ? hv : h;
+  const bool key_f32 = a.key_f32 != 0;
+#pragma unroll
+  for (int p = 0; p < STAGE_PASSES; ++p) {
+    const int idx = p * kVerifyThreads + lane;
+    const int vid = idx / C4, kk = (idx - vid * C4) * 4;
+    if (vid < NV) {
+      const bool is_q = vid >= QM;
+      const float sc = (is_q && !a.l2norm) ? a.scale : 1.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) m_lds[vid][kk + e] = xs[p][e] * sc;
+      const int t = is_q ? vid - QM : vid;
+      if (!is_q && !a.l2norm && key_writer && ((valid_mask >> t) & 1u) && kk < K) {
+        const int64_t base = int64_t(b) * a.key_rs + int64_t(key_head) * a.key_hs + int64_t(t) * a.key_ts + kk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st_f32_or<A>(a.key, base + e, key_f32, xs[p][e]);
+      }
+    }
+  }
+  if (rec_ok && vt == 0 && lane < QM && ((valid_mask >> lane) & 1u))
+    a.decay[int64_t(b) * a.decay_rs + int64_t(hv) * a.decay_hs + int64_t(lane) * a.decay_ts] =
+        expf(ld_f32_or<A>(a.g, (bos + lane) * a.g_ts + hv, a.g_f32 != 0));
+  __syncthreads();
+
+  if (a.l2norm) {
+    // kernels.py:645-648: x * rsqrt(sum(x*x) + 1e-6) for q and k, then q *= scale.
+    if (lane < NV) {
+      float ss = 0.0f;
+      for (int kk = 0; kk < KP; ++kk) ss += m_lds[lane][kk] * m_lds[lane][kk];
+      inv_lds[lane] = rsqrtf(ss + 1e-6f);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < STAGE_PASSES; ++p) {
+      const int idx = p * kVerifyThreads + lane;
+      const int vid = idx / C4, kk = (idx - vid * C4) * 4;
+      if (vid < NV) {
+        const bool is_q = vid >= QM;
+        const int t = is_q ? vid - QM : vid;
+        const bool wr = !is_q && key_writer && ((valid_mask >> t) & 1u) && kk < K;
+        const int64_t base = int64_t(b) * a.key_rs + int64_t(key_head) * a.key_hs + int64_t(t) * a.key_ts + kk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = m_lds[vid][kk + e] * inv_lds[vid];
+          m_lds[vid][kk + e] = x * (is_q ? a.scale : 1.0f);
+          if (wr) st_f32_or<A>(a.key, base + e, key_f32, x);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- 4. Gram matrix k_s . m_j (8 lanes per dot product, DPP sum) ----
+  {
+    const int j8 = lane & 7;
+    for (int d0 = 0; d0 < QM * NV; d0 += kVerifyThreads / 8) {
+      const int d = d0 + (lane >> 3);
+      const int s = d / NV, j = d - (d / NV) * NV;
+      float part = 0.0f;
+      if (d < QM * NV) {
+        constexpr int GL = KP / 8;
+#pragma unroll
+        for (int e = 0; e < GL; ++e) part += m_lds[s][j8 * GL + e] * m_lds[j][j8 * GL + e];
+      }
+      part = dpp_sum8(part);
+      if (d < QM * NV && j8 == 0) gram_lds[s][j] = part;
+    }
+  }
+  // B operands come from LDS per chunk group inside every block: keeping all of
+  // them in registers would cost the occupancy the load pipeline needs. Lanes
+  // of columns >= NV read some valid row: those columns of D are never used.
+  const bool col_live = li < NV;
+  const int brow = li & (NV - 1);
+
+  // ---- 5. pipelined S_0 . [k, q~] on the matrix cores, recurrence per half ----
+  auto gemv_block = [&](int rb, const uint4 (&src)[J]) {
+    asm volatile("" ::: "memory");  // re-read the B operands for every block
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float bop[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) bop[e] = m_lds[brow][E * (4 * j + ls) + e];
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(chunk_elem<S>(src[j], e), bop[e], acc, 0, 0, 0);
+    }
+    if (col_live) {
+      const int rr = (rb & 3) * 16 + 4 * ls;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d_lds[rr + r][li] = acc[r];
+    }
+  };
+  const bool out_f32 = a.out_f32 != 0;
+  auto recurrence = [&](int half) {
+    __syncthreads();  // d_lds (and, on the first half, gram_lds) complete
+    const int lrow = half * 64 + lane;
+    const bool row_ok = row0 + lrow < V;
+    float u[QM], wq[QM];
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      u[t] = d_lds[lane][t];
+      wq[t] = d_lds[lane][QM + t];
+    }
+    float *corr_row = a.corr + int64_t(b) * a.corr_rs + int64_t(hv) * a.corr_hs + row0 + lrow;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      if ((valid_mask >> t) & 1u) {
+        const float d = dec[t];
+        const float c = (vv[half][t] - d * u[t]) * bet[t];
+#pragma unroll
+        for (int j = t + 1; j < QM; ++j) u[j] = __builtin_fmaf(c, gram_lds[t][j], d * u[j]);
+#pragma unroll
+        for (int j = t; j < QM; ++j) wq[j] = __builtin_fmaf(c, gram_lds[t][QM + j], d * wq[j]);
+        if (row_ok) {
+          st_f32_or<A>(a.out, (bos + t) * a.out_ts + out_base + lrow, out_f32, wq[t]);
+          if (rec_ok) corr_row[int64_t(t) * a.corr_ts] = c;
+        }
+      }
+    }
+    __syncthreads();  // d_lds may be overwritten by the next half
+  };
+#pragma unroll
+  for (int rb = 0; rb < NRB; rb += 2) {
+    gemv_block(rb, bufA);
+    if (rb + 2 < NRB && row0 + (rb + 2) * 16 < V) load_block(rb + 2, bufA);
+    gemv_block(rb + 1, bufB);
+    if (rb + 3 < NRB && row0 + (rb + 3) * 16 < V) load_block(rb + 3, bufB);
+    if (rb + 2 == NRB / 2) load_v(1);
+    if ((rb + 2) % 4 == 0 && row0 + (rb - 2) * 16 < V) recurrence((rb + 2) / 4 - 1);
+  }
+}
+
+// Launch for one state type; defined per state type in verify_<state>.hip.
+template <typename S>
+void launch_verify_state(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a);
+
+template <typename S, typename A, int J>
+static void launch_verify_q(int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
+  switch (qm) {
+    case 1: hipLaunchKernelGGL((verify_kernel<S, A, J, 1>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((verify_kernel<S, A, J, 2>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((verify_kernel<S, A, J, 4>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((verify_kernel<S, A, J, 8>), grid, dim3(kVerifyThreads), 0, s, a); break;
+  }
+}
+
+// J: 16-byte chunks per lane per row, KP = 4 * E * J <= 256, so J <= 16 for
+// f32 state and J <= 8 for 16-bit state.
+template <typename S, typename A>
+static void launch_verify_j(int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
+  switch (j) {
+    case 1: launch_verify_q<S, A, 1>(qm, grid, s, a); break;
+    case 2: launch_verify_q<S, A, 2>(qm, grid, s, a); break;
+    case 4: launch_verify_q<S, A, 4>(qm, grid, s, a); break;
+    case 8: launch_verify_q<S, A, 8>(qm, grid, s, a); break;
+    default:
+      if constexpr (Chunk<S>::E == 4) launch_verify_q<S, A, 16>(qm, grid, s, a);
+      break;
+  }
+}
+
+#define GDN_DEFINE_VERIFY_LAUNCH(STATE)                                                                   \
+  template <>                                                                                             \
+  void launch_verify_state<STATE>(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) { \
+    switch (act_dt) {                                                                                     \
+      case GDN_DT_BF16: launch_verify_j<STATE, bf16>(j, qm, grid, s, a); break;                           \
+      case GDN_DT_F16: launch_verify_j<STATE, f16>(j, qm, grid, s, a); break;                             \
+      default: launch_verify_j<STATE, float>(j, qm, grid, s, a); break;                                   \
+    }                                                                                                     \
+  }
+
+}  // namespace gdn
