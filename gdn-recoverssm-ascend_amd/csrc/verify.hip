@@ -60,6 +60,17 @@ extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v
       return GDN_ERR_UNSUPPORTED;
     }
   }
+  // Activations are read through 32-bit offsets from each row's first token.
+  const int64_t act_b = act == GDN_DT_F32 ? 4 : 2;
+  auto window_ok = [Q](int64_t ts, int64_t width, int64_t esz) {
+    return ts >= 0 && ((Q - 1) * ts + width) * esz + 16 < int64_t(kWindowBytes);
+  };
+  if (!window_ok(config[8], heads * K, act_b) || !window_ok(config[9], heads * K, act_b) ||
+      !window_ok(config[10], value_heads * V, act_b) || !window_ok(config[11], value_heads, 4) ||
+      !window_ok(config[12], value_heads, 4)) {
+    set_error("verify: activation token strides must be non-negative and span under 2 GiB per window");
+    return GDN_ERR_UNSUPPORTED;
+  }
   if (rows == 0 || tokens == 0) return GDN_OK;
   if (!q || !k || !v || !g || !beta || !state || !correction || !key || !decay || !out || !qsl || !indices) {
     set_error("verify: null tensor pointer");
@@ -116,13 +127,6 @@ extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v
   a.out_f32 = ext->out_dtype == GDN_DT_F32;
   a.l2norm = ext->qk_l2norm;
   a.key_per_value_head = ext->key_per_value_head;
-  // Four-element activation loads need 4-element alignment of both q and k.
-  const int act_bytes = ext->act_dtype == GDN_DT_F32 ? 4 : 2;
-  const uintptr_t align = uintptr_t(4 * act_bytes);
-  a.vec4 = ((reinterpret_cast<uintptr_t>(q) % align) == 0 && (reinterpret_cast<uintptr_t>(k) % align) == 0 &&
-            a.q_ts % 4 == 0 && a.k_ts % 4 == 0 && K % 4 == 0)
-               ? 1
-               : 0;
   int j = 1;
   while (4 * E * j < K) j *= 2;
   const int qm = Q <= 1 ? 1 : Q <= 2 ? 2 : Q <= 4 ? 4 : 8;

@@ -55,7 +55,7 @@ struct VerifyArgs {
   int32_t K, V, NVT;
   int32_t qsl_i64, idx_i64;                  // index dtypes: 1 for int64
   int32_t g_f32, beta_f32, key_f32, out_f32;  // 1: FP32, 0: activation dtype
-  int32_t l2norm, key_per_value_head, vec4;
+  int32_t l2norm, key_per_value_head;
 };
 
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
@@ -68,12 +68,6 @@ __device__ __forceinline__ float ld_act(const void *p, int64_t i) {
   return to_f32(static_cast<const A *>(p)[i]);
 }
 
-// f32 or activation-typed scalar, chosen by a wave-uniform flag.
-template <typename A>
-__device__ __forceinline__ float ld_f32_or(const void *p, int64_t i, bool f32) {
-  return f32 ? static_cast<const float *>(p)[i] : ld_act<A>(p, i);
-}
-
 template <typename A>
 __device__ __forceinline__ void st_f32_or(void *p, int64_t i, bool f32, float x) {
   if (f32)
@@ -82,27 +76,56 @@ __device__ __forceinline__ void st_f32_or(void *p, int64_t i, bool f32, float x)
     static_cast<A *>(p)[i] = from_f32<A>(x);
 }
 
-// Four consecutive activation elements (one 8- or 16-byte load when aligned).
+// Branch-free loads through buffer resources: an invalid lane passes
+// kOutOfRange and reads zero, so every load of a phase issues back to back and
+// no divergent branch forces a wait on it.
+// Resources start at the wave's first token, so every in-bounds offset is far
+// below kWindowBytes (the host checks window extents against it).
+constexpr int kOutOfRange = 0x7ffff000;
+constexpr int kWindowBytes = 0x7fff0000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t byte_off) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(static_cast<const char *>(p) + byte_off), 0,
+                                           kWindowBytes, 0x00020000);
+}
+
 template <typename A>
-__device__ __forceinline__ void ld4_act(const void *p, int64_t off, bool vec, float *x) {
+__device__ __forceinline__ float bits_to_f32(uint32_t u) {
+  if constexpr (sizeof(A) == 4)
+    return __uint_as_float(u);
+  else
+    return to_f32(__builtin_bit_cast(A, uint16_t(u)));
+}
+
+// One activation element at a byte offset (kOutOfRange reads 0); imm is a
+// constant byte displacement applied only to in-range offsets.
+template <typename A>
+__device__ __forceinline__ float buf_ld_act(__amdgpu_buffer_rsrc_t r, int byte_off, int imm = 0) {
+  if constexpr (sizeof(A) == 4)
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+  else
+    return bits_to_f32<A>(__builtin_amdgcn_raw_buffer_load_b16(r, byte_off + imm, 0, 0));
+}
+
+// Four consecutive activation elements starting at a byte offset: one 16-byte
+// load for FP32 (dword alignment suffices), four 2-byte loads otherwise, which
+// need no alignment beyond the element's.
+template <typename A>
+__device__ __forceinline__ void buf_ld4_act(__amdgpu_buffer_rsrc_t r, int byte_off, float *x) {
   if constexpr (sizeof(A) == 4) {
-    if (vec) {
-      const float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + off);
-      x[0] = f.x, x[1] = f.y, x[2] = f.z, x[3] = f.w;
-      return;
-    }
+    const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+    x[0] = __uint_as_float(u[0]), x[1] = __uint_as_float(u[1]);
+    x[2] = __uint_as_float(u[2]), x[3] = __uint_as_float(u[3]);
   } else {
-    if (vec) {
-      const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const A *>(p) + off);
-      x[0] = to_f32(__builtin_bit_cast(A, uint16_t(u.x & 0xffffu)));
-      x[1] = to_f32(__builtin_bit_cast(A, uint16_t(u.x >> 16)));
-      x[2] = to_f32(__builtin_bit_cast(A, uint16_t(u.y & 0xffffu)));
-      x[3] = to_f32(__builtin_bit_cast(A, uint16_t(u.y >> 16)));
-      return;
-    }
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = ld_act<A>(p, off + i);
+    for (int i = 0; i < 4; ++i) x[i] = buf_ld_act<A>(r, byte_off, i * 2);
+  }
+}
+
+// Wave-uniform 32-bit word through the scalar cache. Only for tensors this
+// kernel never writes; the address is rounded down to a dword.
+__device__ __forceinline__ uint32_t scalar_word(uintptr_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) uint32_t *>(addr & ~uintptr_t(3));
 }
 
 template <typename S>
@@ -120,6 +143,16 @@ template <>
 __device__ __forceinline__ float chunk_elem<f16>(const uint4 &raw, int e) {
   const uint32_t w = (e >> 1) == 0 ? raw.x : (e >> 1) == 1 ? raw.y : (e >> 1) == 2 ? raw.z : raw.w;
   return float(__builtin_bit_cast(f16, uint16_t((e & 1) ? (w >> 16) : (w & 0xffffu))));
+}
+
+// Orders the wave's own LDS writes before its later LDS reads. The workgroup
+// is a single wave and LDS executes a wave's instructions in order, so no
+// s_barrier is needed, and a wave-scope fence does not drain the outstanding
+// global loads the way a workgroup barrier's release fence does.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ int64_t ld_idx(const void *p, int64_t i, bool i64) {
@@ -180,6 +213,8 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   // ---- 1. small loads first: k/q chunks, gates, v of the lane's rows ----
   constexpr int C4 = KP / 4;  // 4-element chunks per vector
   constexpr int STAGE_PASSES = (NV * C4 + kVerifyThreads - 1) / kVerifyThreads;
+  constexpr int AS = int(sizeof(A));
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, bos * a.q_ts * AS), rk = make_rsrc(a.k, bos * a.k_ts * AS);
   float xs[STAGE_PASSES][4];
 #pragma unroll
   for (int p = 0; p < STAGE_PASSES; ++p) {
@@ -188,34 +223,47 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     const bool is_q = vid >= QM;
     const int t = is_q ? vid - QM : vid;
     const bool live = vid < NV && ((valid_mask >> t) & 1u) && kk < K;
-    if (live) {
-      const int64_t off = (bos + t) * (is_q ? a.q_ts : a.k_ts) + int64_t(h) * K + kk;
-      ld4_act<A>(is_q ? a.q : a.k, off, a.vec4 != 0, xs[p]);
+    const int el = t * int(is_q ? a.q_ts : a.k_ts) + h * K + kk;
+    const int off = live ? el * AS : kOutOfRange;
+    if constexpr (C4 * QM % kVerifyThreads == 0) {
+      // Every pass lies wholly inside the k vectors or wholly inside the q ones.
+      buf_ld4_act<A>(p * kVerifyThreads < C4 * QM ? rk : rq, off, xs[p]);
     } else {
-      xs[p][0] = xs[p][1] = xs[p][2] = xs[p][3] = 0.0f;
+      float xq[4], xk[4];
+      buf_ld4_act<A>(rq, is_q ? off : kOutOfRange, xq);
+      buf_ld4_act<A>(rk, is_q ? kOutOfRange : off, xk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xs[p][e] = xq[e] + xk[e];
     }
   }
-  // Gates are wave-uniform: keep them in scalar registers.
-  float dec[QM], bet[QM];
+  // Gates are wave-uniform: scalar loads of the dword holding each one (FP32,
+  // or the 16-bit value at its half), decoded after the state loads issue.
+  // Tokens outside the window read element 0 instead and are discarded.
+  const int gsz = a.g_f32 ? 4 : AS, bsz = a.beta_f32 ? 4 : AS;
+  uint32_t graw[QM], braw[QM];
+  int gsh[QM], bsh[QM];
 #pragma unroll
   for (int t = 0; t < QM; ++t) {
     const bool tv = (valid_mask >> t) & 1u;
-    const int64_t tok = bos + t;
-    const float d = tv ? expf(ld_f32_or<A>(a.g, tok * a.g_ts + hv, a.g_f32 != 0)) : 1.0f;
-    const float be = tv ? ld_f32_or<A>(a.beta, tok * a.beta_ts + hv, a.beta_f32 != 0) : 0.0f;
-    dec[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(d)));
-    bet[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(be)));
+    const uintptr_t ga = reinterpret_cast<uintptr_t>(a.g) + (tv ? uintptr_t(((bos + t) * a.g_ts + hv) * gsz) : 0);
+    const uintptr_t ba =
+        reinterpret_cast<uintptr_t>(a.beta) + (tv ? uintptr_t(((bos + t) * a.beta_ts + hv) * bsz) : 0);
+    gsh[t] = int(ga & 2) * 8;
+    bsh[t] = int(ba & 2) * 8;
+    graw[t] = scalar_word(ga);
+    braw[t] = scalar_word(ba);
   }
   // v of the lane's row in each half; the second half is loaded later, after
   // the loads it must not wait behind.
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v, bos * a.v_ts * AS);
   float vv[2][QM];
   auto load_v = [&](int half) {
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
       const int vr = row0 + half * 64 + lane;
-      vv[half][t] = (vr < V && ((valid_mask >> t) & 1u))
-                        ? ld_act<A>(a.v, (bos + t) * a.v_ts + out_base + half * 64 + lane)
-                        : 0.0f;
+      const bool ok = vr < V && ((valid_mask >> t) & 1u);
+      const int off = ok ? (t * int(a.v_ts) + int(out_base) + half * 64 + lane) * AS : kOutOfRange;
+      vv[half][t] = buf_ld_act<A>(rv, off);
     }
   };
   load_v(0);
@@ -250,6 +298,15 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   uint4 bufA[J], bufB[J];
   load_block(0, bufA);
   load_block(1, bufB);
+  float dec[QM], bet[QM];
+#pragma unroll
+  for (int t = 0; t < QM; ++t) {
+    const bool tv = (valid_mask >> t) & 1u;
+    const float gv = a.g_f32 ? __uint_as_float(graw[t]) : bits_to_f32<A>((graw[t] >> gsh[t]) & 0xffffu);
+    const float bv = a.beta_f32 ? __uint_as_float(braw[t]) : bits_to_f32<A>((braw[t] >> bsh[t]) & 0xffffu);
+    dec[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? expf(gv) : 1.0f)));
+    bet[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? bv : 0.0f)));
+  }
 
   // ---- 3. stage vectors and records ----
   const bool rec_ok = b < a.record_rows;
@@ -273,10 +330,14 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       }
     }
   }
-  if (rec_ok && vt == 0 && lane < QM && ((valid_mask >> lane) & 1u))
-    a.decay[int64_t(b) * a.decay_rs + int64_t(hv) * a.decay_hs + int64_t(lane) * a.decay_ts] =
-        expf(ld_f32_or<A>(a.g, (bos + lane) * a.g_ts + hv, a.g_f32 != 0));
-  __syncthreads();
+  if (rec_ok && vt == 0) {
+    float dl = 1.0f;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) dl = lane == t ? dec[t] : dl;
+    if (lane < QM && ((valid_mask >> lane) & 1u))
+      a.decay[int64_t(b) * a.decay_rs + int64_t(hv) * a.decay_hs + int64_t(lane) * a.decay_ts] = dl;
+  }
+  wave_lds_sync();
 
   if (a.l2norm) {
     // kernels.py:645-648: x * rsqrt(sum(x*x) + 1e-6) for q and k, then q *= scale.
@@ -285,7 +346,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       for (int kk = 0; kk < KP; ++kk) ss += m_lds[lane][kk] * m_lds[lane][kk];
       inv_lds[lane] = rsqrtf(ss + 1e-6f);
     }
-    __syncthreads();
+    wave_lds_sync();
 #pragma unroll
     for (int p = 0; p < STAGE_PASSES; ++p) {
       const int idx = p * kVerifyThreads + lane;
@@ -303,7 +364,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         }
       }
     }
-    __syncthreads();
+    wave_lds_sync();
   }
 
   // ---- 4. Gram matrix k_s . m_j (8 lanes per dot product, DPP sum) ----
@@ -349,7 +410,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   };
   const bool out_f32 = a.out_f32 != 0;
   auto recurrence = [&](int half) {
-    __syncthreads();  // d_lds (and, on the first half, gram_lds) complete
+    wave_lds_sync();  // d_lds (and, on the first half, gram_lds) complete
     const int lrow = half * 64 + lane;
     const bool row_ok = row0 + lrow < V;
     float u[QM], wq[QM];
@@ -374,7 +435,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         }
       }
     }
-    __syncthreads();  // d_lds may be overwritten by the next half
+    wave_lds_sync();  // d_lds may be overwritten by the next half
   };
 #pragma unroll
   for (int rb = 0; rb < NRB; rb += 2) {
