@@ -44,10 +44,55 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="align_b256")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-only", action="store_true", help="skip the per-kernel event pass")
+    ap.add_argument("--kernel-only", action="store_true", help="skip the separate conv-compaction timing")
     ap.add_argument("--copy-calibration", type=int, default=0,
                     help="also run a device copy of this many MiB (PMC scale calibration)")
     return ap.parse_args()
+
+
+class _HipTimer:
+    """HIP events created with hipEventDisableSystemFence, recorded on the
+    given stream (torch's Event API does not expose creation flags). Uses the
+    HIP runtime torch already loaded."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, stream_handle):
+        import ctypes
+
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        if path is None:
+            raise RuntimeError("HIP runtime not loaded")
+        self._ct = ctypes
+        self._hip = ctypes.CDLL(path)
+        self._stream = ctypes.c_void_p(stream_handle)
+        self._events = []
+
+    def event(self):
+        ev = self._ct.c_void_p()
+        if self._hip.hipEventCreateWithFlags(self._ct.byref(ev), self._ct.c_uint(self.DISABLE_SYSTEM_FENCE)) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+        self._events.append(ev)
+        return ev
+
+    def record(self, ev):
+        if self._hip.hipEventRecord(ev, self._stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed(self, a, b):
+        ms = self._ct.c_float()
+        if self._hip.hipEventElapsedTime(self._ct.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self):
+        for ev in getattr(self, "_events", []):
+            self._hip.hipEventDestroy(ev)
 
 
 def byte_model(w, plan_lens, plan_final, plan_boundary, plan_blen):
@@ -82,6 +127,26 @@ def byte_model(w, plan_lens, plan_final, plan_boundary, plan_blen):
     commit = state_pages * HV * V * K * 4 + int(n[active].sum()) * (HV * V * 4 + H * K * 2 + HV * 4) + 52 * B
     return dict(verify=verify, commit=commit, tokens=T, active_rows=int(active.sum()),
                 boundary_writes=int(store_b.sum()), accepted_tokens=int(n[active].sum()))
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE, scaled by the copy-kernel calibration
+    recorded with them), or None when no summary matches this workload and
+    these kernel sources."""
+    from gdn_recoverssm_ascend import _build
+
+    path = os.path.join(HERE, "profiles", f"pmc_traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None, f"no PMC summary for {workload}"
+    with open(path) as f:
+        prof = json.load(f)
+    if prof.get("sources_sha1") != _build.source_digest():
+        return None, f"{os.path.relpath(path, HERE)} was taken of other kernel sources"
+    k = prof.get("kernels", {}).get(kernel)
+    if not k:
+        return None, f"{os.path.relpath(path, HERE)} has no {kernel} entry"
+    return k["hbm_bytes"], os.path.relpath(path, HERE)
 
 
 def cpu_baseline(w_cpu, threads):
@@ -151,28 +216,47 @@ def main():
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
+    timer = _HipTimer(stream.cuda_stream)
+
+    # Timed region 1: K plain steps -> value and ms_per_step.
+    t0, t1 = timer.event(), timer.event()
     torch.cuda.synchronize()
-    t_start.record(stream)
+    timer.record(t0)
     for _ in range(args.steps):
         step()
-    t_end.record(stream)
+    timer.record(t1)
     torch.cuda.synchronize()
-    step_ms = t_start.elapsed_time(t_end) / args.steps
+    step_ms = timer.elapsed(t0, t1) / args.steps
 
-    # Per-kernel durations (HIP events around each launch on the same stream).
-    kernel_ms = {}
+    # Timed region 2: the same K steps with an event between consecutive
+    # launches, on the stream the kernels run on -> per-kernel durations.
+    # The events skip the system-scope fence, so they neither flush the
+    # caches nor hold the next launch back.
+    names = [sp.name for sp in step_specs]
+    marks = [[timer.event() for _ in range(len(step_specs) + 1)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        ev = marks[i]
+        timer.record(ev[0])
+        for j, sp in enumerate(step_specs):
+            sp.launch()
+            timer.record(ev[j + 1])
+    torch.cuda.synchronize()
+    marked_step_ms = timer.elapsed(marks[0][0], marks[-1][-1]) / args.steps
+    kernel_ms = {n: sum(timer.elapsed(ev[j], ev[j + 1]) for ev in marks) / args.steps for j, n in enumerate(names)}
+
+    # Conv-state compaction runs in the same commit but is outside the byte
+    # model; timed on its own after the region.
     if not args.kernel_only:
         reps = max(10, args.steps // 2)
-        for sp in step_specs + [by_name["conv"]]:
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-            for a, b in ev:
-                a.record(stream)
-                sp.launch()
-                b.record(stream)
-            torch.cuda.synchronize()
-            kernel_ms[sp.name] = sum(a.elapsed_time(b) for a, b in ev) / reps
+        conv = by_name["conv"]
+        ev = [(timer.event(), timer.event()) for _ in range(reps)]
+        for a, b in ev:
+            timer.record(a)
+            conv.launch()
+            timer.record(b)
+        torch.cuda.synchronize()
+        kernel_ms["conv"] = sum(timer.elapsed(a, b) for a, b in ev) / reps
 
     nbytes = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
     total = nbytes["verify"] + nbytes["commit"]
@@ -187,6 +271,7 @@ def main():
         per_kernel[name] = entry
     dominant = max(("verify", "fold"), key=lambda n: kernel_ms.get(n, 0.0)) if kernel_ms else "fold"
     dk = per_kernel.get(dominant, {})
+    traffic, traffic_src = measured_traffic(s.name, dominant)
     roofline = {
         "kernel": dominant,
         "bound": "hbm",
@@ -194,7 +279,8 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": dk.get("frac"),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": traffic_src,
         "algorithmic_bytes": dk.get("bytes"),
         "avg_us": dk.get("us"),
     }
@@ -230,6 +316,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 4),
         "us_per_step": round(step_ms * 1e3, 2),
+        "us_per_step_with_kernel_events": round(marked_step_ms * 1e3, 2),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",

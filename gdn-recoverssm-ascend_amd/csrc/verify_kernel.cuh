@@ -269,9 +269,9 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   load_v(0);
 
   // ---- 2. first two state blocks ----
-  // Buffer loads: one resource per (slot, head) tile, a 32-bit per-lane offset,
-  // the block step in soffset and the chunk step in the immediate. Rows >= V
-  // lie past the resource's extent and read as zero; so do chunks >= K.
+  // Buffer loads: one resource per (slot, head) tile, a 32-bit per-lane offset
+  // per chunk and the block step in soffset. Rows >= V lie past the resource's
+  // extent and read as zero; chunks >= K get an out-of-range offset.
   // Rows of block rb: rb*16 + li; the lane loads chunks 4j + ls of its row.
   const S *sp = static_cast<const S *>(a.state) + slot * a.state_bs + int64_t(hv) * a.state_hs +
                 int64_t(row0) * a.state_vs;
@@ -280,23 +280,20 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       const_cast<S *>(sp), 0, tile_rows * a.state_vs * int(sizeof(S)), 0x00020000);
   const int row_bytes = a.state_vs * int(sizeof(S));
   const int lane_off = li * row_bytes + ls * 16;
-  const bool full_k = K == KP;  // no chunk past K: plain offsets, chunk step in the immediate
+  // One form for every K, and every block is loaded (blocks past V read as
+  // zero): a conditional load would leave a path on which it was not issued,
+  // and the wait counts of every later MFMA would have to assume that path,
+  // draining the pipeline at each block.
   auto load_block = [&](int rb, uint4 (&dst)[J]) {
-    if (full_k) {
 #pragma unroll
-      for (int j = 0; j < J; ++j)
-        dst[j] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off + j * 64, rb * 16 * row_bytes, 0));
-    } else {
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : 0x7ffff000;
-        dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
-      }
+    for (int j = 0; j < J; ++j) {
+      const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
+      dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
     }
   };
   uint4 bufA[J], bufB[J];
   load_block(0, bufA);
+  __builtin_amdgcn_sched_barrier(0);  // keep block 0's loads ahead of block 1's
   load_block(1, bufB);
   float dec[QM], bet[QM];
 #pragma unroll
@@ -440,9 +437,9 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 #pragma unroll
   for (int rb = 0; rb < NRB; rb += 2) {
     gemv_block(rb, bufA);
-    if (rb + 2 < NRB && row0 + (rb + 2) * 16 < V) load_block(rb + 2, bufA);
+    if (rb + 2 < NRB) load_block(rb + 2, bufA);
     gemv_block(rb + 1, bufB);
-    if (rb + 3 < NRB && row0 + (rb + 3) * 16 < V) load_block(rb + 3, bufB);
+    if (rb + 3 < NRB) load_block(rb + 3, bufB);
     if (rb + 2 == NRB / 2) load_v(1);
     if ((rb + 2) % 4 == 0 && row0 + (rb - 2) * 16 < V) recurrence((rb + 2) / 4 - 1);
   }

@@ -9,6 +9,7 @@ at run time.
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -28,6 +29,18 @@ ARCH = os.environ.get("GDN_OFFLOAD_ARCH", "gfx950")
 
 def sources() -> list[str]:
     return sorted(os.path.join(CSRC_DIR, f) for f in os.listdir(CSRC_DIR) if f.endswith(".hip"))
+
+
+def source_digest() -> str:
+    """SHA-1 over the kernel sources and the C header: identifies the code a
+    profile was taken of."""
+    h = hashlib.sha1()
+    files = sorted(f for f in os.listdir(CSRC_DIR) if f.endswith((".hip", ".cuh")))
+    for path in [os.path.join(CSRC_DIR, f) for f in files] + [os.path.join(INCLUDE_DIR, "gdn_recoverssm_hip.h")]:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def hipcc() -> str:
