@@ -15,7 +15,7 @@ sees under speculative decoding:
 | name              | layers | rows | H  | HV | K=V | Q | mode  | accept    |
 |-------------------|--------|------|----|----|-----|---|-------|-----------|
 | plumbing_b4       | 1      | 4    | 2  | 4  | 64  | 4 | none  | uniform   |
-| qwen3next_b64     | 1      | 64   | 16 | 32 | 128 | 4 | none  | uniform   |
+| pool512_b64       | 1      | 64   | 16 | 32 | 128 | 4 | none  | uniform   |
 | align_b256        | 1      | 256  | 16 | 32 | 128 | 4 | align | uniform   |
 | decode_q1_b256    | 1      | 256  | 16 | 32 | 128 | 1 | none  | all       |
 | skewed_q8_b256    | 1      | 256  | 16 | 32 | 128 | 8 | none  | geometric |
@@ -56,7 +56,7 @@ class WorkloadSpec:
 
 SPECS = {
     "plumbing_b4": WorkloadSpec("plumbing_b4", 1, 4, 2, 4, 64, 64, 4),
-    "qwen3next_b64": WorkloadSpec("qwen3next_b64", 1, 64, 16, 32, 128, 128, 4, pool_pages=512),
+    "pool512_b64": WorkloadSpec("pool512_b64", 1, 64, 16, 32, 128, 128, 4, pool_pages=512),
     "align_b256": WorkloadSpec("align_b256", 1, 256, 16, 32, 128, 128, 4, align=True, padded_rows=6),
     "decode_q1_b256": WorkloadSpec("decode_q1_b256", 1, 256, 16, 32, 128, 128, 1, accept="all", pool_pages=512),
     "skewed_q8_b256": WorkloadSpec("skewed_q8_b256", 1, 256, 16, 32, 128, 128, 8, accept="geometric", pool_pages=512),

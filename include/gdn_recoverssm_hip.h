@@ -55,7 +55,7 @@ extern "C" {
  * (csrc/ops.cpp:100-141): dimensions, dtypes and layout flags that the
  * reference's Triton kernel took as constexprs (kernels.py:534-545). */
 typedef struct gdn_verify_ext {
-  int64_t key_dim;          /* K (<= 256, multiple of 8) */
+  int64_t key_dim;          /* K (<= 256; a multiple of 4 for FP32 state, of 8 for 16-bit state) */
   int64_t value_dim;        /* V (>= 1) */
   int32_t act_dtype;        /* q, k, v, out: F32 / BF16 / F16 */
   int32_t beta_dtype;       /* activation dtype or F32 */

@@ -175,7 +175,7 @@ def test_empty_batch_returns_without_launch(dev):
     assert out.shape == (1, 0, 2, 128)
 
 
-@pytest.mark.parametrize("name,rows", [("qwen3next_b64", None), ("align_b256", 40), ("decode_q1_b256", 40),
+@pytest.mark.parametrize("name,rows", [("pool512_b64", None), ("align_b256", 40), ("decode_q1_b256", 40),
                                        ("skewed_q8_b256", 24)])
 def test_baseline_workloads(dev, name, rows):
     """Full-size launches; the oracle checks a seeded subset of rows."""
@@ -224,3 +224,43 @@ def test_baseline_workloads(dev, name, rows):
     keys = rec.key[sel_t].cpu()
     mk = res.record_written[:, None, :, None].expand_as(keys)
     assert torch.equal(keys[mk].float(), res.key[mk].float())
+
+
+def test_verify_graph_replay(dev):
+    """A verify launch recorded in a HIP graph: every replay, with eager work
+    in between, reproduces the eager launch bit for bit."""
+    P = _problem(6, 2, 4, 128, 128, 4, qlens=[4, 3, 4, 2, 0, 4], null_rows=(1,))
+    inp, B, H, HV, K, V, Q, T = P["inp"], P["B"], P["H"], P["HV"], P["K"], P["V"], P["Q"], P["T"]
+    q, k, v, g, beta = (t.to(dev) for t in (inp.q, inp.k, inp.v, inp.g, inp.beta))
+    ckpt, qsl, idx = P["ckpt"].to(dev), P["qsl"].to(dev), P["idx"].to(dev)
+    rec = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=k.dtype)
+    out = torch.empty(1, T, HV, V, dtype=v.dtype, device=dev)
+
+    def run():
+        gdn_recoverssm_verify(g, beta, q, k, v, checkpoint_state=ckpt, replay_cache=rec, query_start_loc=qsl,
+                              state_indices=idx, spec_query_len=Q, out=out)
+
+    def reset():
+        for t in (out, rec.correction, rec.key, rec.decay):
+            t.fill_(SENT)
+
+    reset()
+    run()
+    torch.cuda.synchronize()
+    want = [t.clone() for t in (out, rec.correction, rec.key, rec.decay)]
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()  # warm the launch path on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        run()
+    for _ in range(3):
+        reset()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip((out, rec.correction, rec.key, rec.decay), want):
+            assert torch.equal(got, ref), "graph replay differs from the eager launch"
