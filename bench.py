@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="align_b256")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--loop-steps", type=int, default=None,
+                    help="decode-loop workloads: speculative steps to time (default: the workload's own)")
     ap.add_argument("--kernel-only", action="store_true", help="skip the separate conv-compaction timing")
     ap.add_argument("--copy-calibration", type=int, default=0,
                     help="also run a device copy of this many MiB (PMC scale calibration)")
@@ -173,12 +175,166 @@ def cpu_baseline(w_cpu, threads):
     return time.perf_counter() - t0
 
 
+def commit_bytes(spec, n, fin, bnd, blen, num_pages):
+    """Algorithmic bytes of one layer's fold for plan rows (n, final, boundary,
+    boundary length); same model as ``byte_model``'s commit part."""
+    HV, H, K, V = spec.value_heads, spec.key_heads, spec.key_dim, spec.value_dim
+    active = n > 0
+    store_b = active & (bnd > 0) & (bnd < num_pages) & (bnd != fin) & (blen > 0) & (blen <= n)
+    pages = int(active.sum()) * 2 + int(store_b.sum())
+    return pages * HV * V * K * 4 + int(n[active].sum()) * (HV * V * 4 + H * K * 2 + HV * 4)
+
+
+def conv_bytes(spec, n, bnd, blen, num_pages, conv_dim, history, elem):
+    """Conv-state compaction bytes of one layer: per committed row, `history`
+    positions of every channel read and written to the final slot, and again
+    to the boundary slot when one is written."""
+    active = n > 0
+    store_b = active & (bnd > 0) & (bnd < num_pages) & (blen >= 1)
+    return (int(active.sum()) * 2 + int(store_b.sum()) * 2) * conv_dim * history * elem
+
+
+def decode_loop(args):
+    """The decode-loop workload: every layer's verify, then one commit (plan,
+    conv compaction, fold) across all layers, per speculative step, with the
+    state carried from step to step (C += n, the source page becomes the final
+    page) and fresh accepted lengths each step."""
+    import torch
+
+    from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = W.make_workload(args.workload, gen_device="cuda").to(dev)
+    s = w.spec
+    L, B, Q, H, HV, K, V = s.layers, s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+    steps = s.steps if args.loop_steps is None else args.loop_steps
+    m = w.meta
+    recs = [ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=w.inputs[0].k.dtype)
+            for _ in range(L)]
+    ctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, recs, spec_query_len=Q, max_num_reqs=B)
+    state_idx = m.state_indices.clone()
+    computed = m.num_computed.clone()
+    accepted = torch.zeros(B, dtype=torch.int32, device=dev)
+    gen = torch.Generator().manual_seed(7)
+    acc_all = torch.stack([W.sample_accepted(s, B, gen) for _ in range(steps + args.warmup)]).to(dev)
+    outs = [torch.empty(1, w.tokens, HV, V, dtype=w.inputs[0].v.dtype, device=dev) for _ in range(L)]
+    verify_specs: list = []
+    for layer in range(L):
+        inp = w.inputs[layer]
+        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[layer],
+                              replay_cache=recs[layer], query_start_loc=m.query_start_loc, state_indices=state_idx,
+                              spec_query_len=Q, out=outs[layer], _collect=verify_specs)
+    commit_specs = ctx.make_commit_specs(accepted, state_idx, m.query_start_loc, block_table=m.block_table,
+                                         num_computed_tokens=computed, mamba_block_size=m.block_size, commit_conv=True)
+    lens, fin, bnd, blen = (ctx.commit_lens[:B], ctx.final_state_indices[:B], ctx.boundary_state_indices[:B],
+                            ctx.boundary_recovery_lens[:B])
+    hist_lens = torch.empty(steps, 4, B, dtype=torch.int32, device=dev)
+
+    def step(i, record=None):
+        accepted.copy_(acc_all[i])
+        for sp in verify_specs:
+            sp.launch()
+        for sp in commit_specs:
+            sp.launch()
+        if record is not None:
+            for j, t in enumerate((lens, fin, bnd, blen)):
+                hist_lens[record, j].copy_(t)
+        committed = lens > 0
+        computed.add_(lens.to(computed.dtype))
+        state_idx.copy_(torch.where(committed, fin.to(state_idx.dtype), state_idx))
+
+    start_idx, start_c = state_idx.clone(), computed.clone()
+    for i in range(args.warmup):
+        step(steps + i)
+    torch.cuda.synchronize()
+    state_idx.copy_(start_idx)
+    computed.copy_(start_c)
+    stream = torch.cuda.current_stream(dev)
+    timer = _HipTimer(stream.cuda_stream)
+    t0, t1 = timer.event(), timer.event()
+    torch.cuda.synchronize()
+    timer.record(t0)
+    for i in range(steps):
+        step(i, record=i)
+    timer.record(t1)
+    torch.cuda.synchronize()
+    total_ms = timer.elapsed(t0, t1)
+
+    # Per-phase split over a second pass of the same steps (state restarted).
+    state_idx.copy_(start_idx)
+    computed.copy_(start_c)
+    ev = [(timer.event(), timer.event(), timer.event()) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        a, b, c = ev[i]
+        accepted.copy_(acc_all[i])
+        timer.record(a)
+        for sp in verify_specs:
+            sp.launch()
+        timer.record(b)
+        for sp in commit_specs:
+            sp.launch()
+        timer.record(c)
+        committed = lens > 0
+        computed.add_(lens.to(computed.dtype))
+        state_idx.copy_(torch.where(committed, fin.to(state_idx.dtype), state_idx))
+    torch.cuda.synchronize()
+    verify_ms = sum(timer.elapsed(a, b) for a, b, _ in ev) / steps
+    commit_ms = sum(timer.elapsed(b, c) for _, b, c in ev) / steps
+
+    nb = byte_model(w, lens, fin, bnd, blen)  # verify part is the same every step
+    verify_b = nb["verify"] * L
+    hl = hist_lens.cpu().long()
+    conv_dim, conv_len = w.conv_states[0].shape[1:]
+    hist = conv_len - Q + 1
+    commit_b = conv_b = 0
+    tokens_committed = 0
+    for i in range(steps):
+        n_, f_, b_, bl_ = hl[i]
+        commit_b += commit_bytes(s, n_, f_, b_, bl_, w.num_pages) * L + 52 * B
+        conv_b += conv_bytes(s, n_, b_, bl_, w.num_pages, conv_dim, hist, w.conv_states[0].element_size()) * L
+        tokens_committed += int(n_[n_ > 0].sum())
+    step_ms = total_ms / steps
+    total_b = verify_b * steps + commit_b + conv_b
+    gbs = total_b / (total_ms * 1e-3) / 1e9
+    line = {
+        "metric": f"decode loop: {L} GDN layers verify + one grouped commit per step, B={B} Q={Q}, state carried",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "us_per_step": round(step_ms * 1e3, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": s.name, "layers": L, "rows": B, "key_heads": H, "value_heads": HV, "key_dim": K,
+                   "value_dim": V, "window": Q, "mode": "align", "block_size": m.block_size, "pages_per_layer": w.num_pages},
+        "phases_us_per_step": {"verify_all_layers": round(verify_ms * 1e3, 1), "commit": round(commit_ms * 1e3, 1)},
+        "bytes_per_step": {"verify": verify_b, "commit": round(commit_b / steps), "conv": round(conv_b / steps)},
+        "tokens_committed_per_step": round(tokens_committed / steps, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
               "(the verify/commit path shards by rows and heads with no exchange; see DESIGN.md)", file=sys.stderr)
         return 2
+    sys.path.insert(0, os.path.join(HERE, "gdn-recoverssm-ascend_amd"))
+    from gdn_recoverssm_ascend import workloads as W
+
+    if W.get_spec(args.workload).layers > 1:
+        return decode_loop(args)
     import torch
 
     from gdn_recoverssm_ascend import workloads as W
