@@ -101,7 +101,37 @@ __global__ __launch_bounds__(64) void plan_kernel(PlanArgs a) {
   }
 }
 
-template <typename E>
+// Conv-state compaction. One workgroup per (layer, row, tile of
+// kConvChannelsPerThread * 256 channels); thread t handles channels
+// tile_base + i*256 + t, so every wave instruction covers consecutive
+// channels.
+//
+// WDW > 0: a channel's window is WDW dwords (<= 16 bytes). When the layer's
+// windows are contiguous (token stride 1, dim stride = window, dword-aligned)
+// the whole window moves as one 128-bit value: the source window is read once
+// for both the final and the boundary history, and each destination window is
+// read and written whole, its positions from `history` on carried over
+// unchanged, so no written line is left half-written. Other layouts (and
+// WDW = 0) use element accesses. All loads of a channel precede its stores, so
+// source, final and boundary slots may alias (boundary stored before final, as
+// kernels.py:1146-1169).
+constexpr int kConvChannelsPerThread = 4;
+
+template <int WDW>
+__device__ __forceinline__ unsigned __int128 conv_load_window(const uint32_t *p) {
+  unsigned __int128 w = 0;
+#pragma unroll
+  for (int j = 0; j < WDW; ++j) w |= static_cast<unsigned __int128>(p[j]) << (32 * j);
+  return w;
+}
+
+template <int WDW>
+__device__ __forceinline__ void conv_store_window(uint32_t *p, unsigned __int128 w) {
+#pragma unroll
+  for (int j = 0; j < WDW; ++j) p[j] = static_cast<uint32_t>(w >> (32 * j));
+}
+
+template <typename E, int WDW>
 __global__ __launch_bounds__(256) void conv_compact_kernel(
     const int64_t *__restrict__ addrs, const int64_t *__restrict__ block_strides,
     const int64_t *__restrict__ dim_strides, const int64_t *__restrict__ token_strides, const void *source,
@@ -114,8 +144,6 @@ __global__ __launch_bounds__(256) void conv_compact_kernel(
   const int64_t tile = wg % dim_tiles;
   const int64_t row = (wg / dim_tiles) % rows;
   const int64_t layer = wg / (dim_tiles * rows);
-  const int64_t d = tile * blockDim.x + threadIdx.x;
-  if (d >= conv_dim) return;
   const int64_t plan_row = (layer_groups ? int64_t(layer_groups[layer]) * cap : 0) + row;
   const int64_t src = load_index(source, plan_row * source_stride, source_dtype);
   const int64_t n = lengths[plan_row];
@@ -123,28 +151,62 @@ __global__ __launch_bounds__(256) void conv_compact_kernel(
   if (!(src > null_block && src < num_blocks && n >= 1 && n - 1 + history <= window && fin > null_block &&
         fin < num_blocks))
     return;
-  E *base = reinterpret_cast<E *>(addrs[layer]);
-  const int64_t bs = block_strides[layer], ds = dim_strides[layer], ts = token_strides[layer];
-  const E *sp = base + src * bs + d * ds;
-  constexpr int kMaxHist = 16;
-  E fv[kMaxHist], bv[kMaxHist];
-  const int64_t hist = history;  // host checks history <= kMaxHist
-  for (int64_t h = 0; h < hist; ++h) fv[h] = sp[(n - 1 + h) * ts];
+  int64_t bidx = null_block, blen = 0;
   bool store_b = false;
-  int64_t bidx = null_block;
   if (align) {
     bidx = boundaries[plan_row];
-    const int64_t blen = boundary_lens[plan_row];
+    blen = boundary_lens[plan_row];
     store_b = bidx > null_block && bidx < num_blocks && blen >= 1 && blen - 1 + history <= window;
+  }
+  E *base = reinterpret_cast<E *>(addrs[layer]);
+  const int64_t bs = block_strides[layer], ds = dim_strides[layer], ts = token_strides[layer];
+  const int64_t c0 = tile * (kConvChannelsPerThread * 256) + threadIdx.x;
+  if constexpr (WDW > 0) {
+    constexpr int EB = int(sizeof(E));
+    if (ts == 1 && ds == window && window * EB == 4 * WDW && (bs * EB) % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(base) & 3u) == 0) {
+      const uint32_t *sp = reinterpret_cast<const uint32_t *>(base + src * bs);
+      uint32_t *fp = reinterpret_cast<uint32_t *>(base + fin * bs);
+      uint32_t *bp = reinterpret_cast<uint32_t *>(base + (store_b ? bidx : fin) * bs);
+      const int hbits = int(history) * EB * 8;  // <= 128: history <= window
+      const unsigned __int128 hmask =
+          hbits >= 128 ? ~static_cast<unsigned __int128>(0) : ((static_cast<unsigned __int128>(1) << hbits) - 1);
+      const int fsh = int(n - 1) * EB * 8, bsh = int(blen > 0 ? blen - 1 : 0) * EB * 8;
+#pragma unroll
+      for (int i = 0; i < kConvChannelsPerThread; ++i) {
+        const int64_t c = c0 + int64_t(i) * 256;
+        if (c < conv_dim) {
+          const unsigned __int128 sw = conv_load_window<WDW>(sp + c * WDW);
+          unsigned __int128 fw = conv_load_window<WDW>(fp + c * WDW);
+          unsigned __int128 bw = 0;
+          if (store_b) bw = conv_load_window<WDW>(bp + c * WDW);
+          fw = (fw & ~hmask) | ((sw >> fsh) & hmask);
+          if (store_b) {
+            bw = (bw & ~hmask) | ((sw >> bsh) & hmask);
+            conv_store_window<WDW>(bp + c * WDW, bw);
+          }
+          conv_store_window<WDW>(fp + c * WDW, fw);
+        }
+      }
+      return;
+    }
+  }
+  constexpr int kMaxHist = 16;
+  for (int i = 0; i < kConvChannelsPerThread; ++i) {
+    const int64_t d = c0 + int64_t(i) * 256;
+    if (d >= conv_dim) break;
+    const E *sp = base + src * bs + d * ds;
+    E fv[kMaxHist], bv[kMaxHist];
+    for (int64_t h = 0; h < history; ++h) fv[h] = sp[(n - 1 + h) * ts];
     if (store_b)
-      for (int64_t h = 0; h < hist; ++h) bv[h] = sp[(blen - 1 + h) * ts];
+      for (int64_t h = 0; h < history; ++h) bv[h] = sp[(blen - 1 + h) * ts];
+    if (store_b) {
+      E *bp = base + bidx * bs + d * ds;
+      for (int64_t h = 0; h < history; ++h) bp[h * ts] = bv[h];
+    }
+    E *fp = base + fin * bs + d * ds;
+    for (int64_t h = 0; h < history; ++h) fp[h * ts] = fv[h];
   }
-  if (store_b) {
-    E *bp = base + bidx * bs + d * ds;
-    for (int64_t h = 0; h < hist; ++h) bp[h * ts] = bv[h];
-  }
-  E *fp = base + fin * bs + d * ds;
-  for (int64_t h = 0; h < hist; ++h) fp[h * ts] = fv[h];
 }
 
 __global__ __launch_bounds__(64) void publish_kernel(const int64_t *__restrict__ desc, int64_t num_buckets,
@@ -291,23 +353,36 @@ extern "C" int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int6
     return GDN_ERR_UNSUPPORTED;
   }
   if (num_rows == 0) return GDN_OK;
-  const int64_t tiles = (conv_dim + 255) / 256;
+  const int64_t per_wg = int64_t(kConvChannelsPerThread) * 256;
+  const int64_t tiles = (conv_dim + per_wg - 1) / per_wg;
   const int64_t grid = tiles * num_rows * num_layers;
   if (grid > 0x7fffffffLL) {
     set_error("conv_compact: grid too large");
     return GDN_ERR_UNSUPPORTED;
   }
   auto s = static_cast<hipStream_t>(stream);
-  if (element_bytes == 2)
-    hipLaunchKernelGGL(conv_compact_kernel<uint16_t>, dim3(unsigned(grid)), dim3(256), 0, s, conv_addrs,
-                       conv_block_strides, conv_dim_strides, conv_token_strides, source, source_dtype,
-                       source_stride, lengths, final_indices, boundary_indices, boundary_lengths, layer_groups,
-                       plan_capacity, null_block, num_rows, conv_dim, history, window, num_blocks, align, tiles);
-  else
-    hipLaunchKernelGGL(conv_compact_kernel<uint32_t>, dim3(unsigned(grid)), dim3(256), 0, s, conv_addrs,
-                       conv_block_strides, conv_dim_strides, conv_token_strides, source, source_dtype,
-                       source_stride, lengths, final_indices, boundary_indices, boundary_lengths, layer_groups,
-                       plan_capacity, null_block, num_rows, conv_dim, history, window, num_blocks, align, tiles);
+  // Dwords per channel window when it fits the 128-bit fast path, else 0.
+  const int64_t wbytes = window * element_bytes;
+  const int wdw = (wbytes % 4 == 0 && wbytes <= 16) ? int(wbytes / 4) : 0;
+#define GDN_CONV_ARGS                                                                                          \
+  conv_addrs, conv_block_strides, conv_dim_strides, conv_token_strides, source, source_dtype, source_stride, \
+      lengths, final_indices, boundary_indices, boundary_lengths, layer_groups, plan_capacity, null_block,    \
+      num_rows, conv_dim, history, window, num_blocks, align, tiles
+#define GDN_CONV_LAUNCH(E)                                                                                  \
+  switch (wdw) {                                                                                            \
+    case 1: hipLaunchKernelGGL((conv_compact_kernel<E, 1>), dim3(unsigned(grid)), dim3(256), 0, s, GDN_CONV_ARGS); break; \
+    case 2: hipLaunchKernelGGL((conv_compact_kernel<E, 2>), dim3(unsigned(grid)), dim3(256), 0, s, GDN_CONV_ARGS); break; \
+    case 3: hipLaunchKernelGGL((conv_compact_kernel<E, 3>), dim3(unsigned(grid)), dim3(256), 0, s, GDN_CONV_ARGS); break; \
+    case 4: hipLaunchKernelGGL((conv_compact_kernel<E, 4>), dim3(unsigned(grid)), dim3(256), 0, s, GDN_CONV_ARGS); break; \
+    default: hipLaunchKernelGGL((conv_compact_kernel<E, 0>), dim3(unsigned(grid)), dim3(256), 0, s, GDN_CONV_ARGS); break; \
+  }
+  if (element_bytes == 2) {
+    GDN_CONV_LAUNCH(uint16_t)
+  } else {
+    GDN_CONV_LAUNCH(uint32_t)
+  }
+#undef GDN_CONV_LAUNCH
+#undef GDN_CONV_ARGS
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     set_error("conv_compact: launch failed: %s", hipGetErrorString(err));

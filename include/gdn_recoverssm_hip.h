@@ -103,7 +103,9 @@ int gdn_recoverssm_verify(const void *q, const void *k, const void *v, const voi
  * int32 layer_groups [layers] (may be NULL: every layer uses group 0), and the
  * int32 plan arrays [groups * plan_capacity]. state_ref/correction_ref/key_ref/
  * decay_ref are the first layer's tensors (unused for addressing, as in the
- * reference, csrc/fold.h:253-273). */
+ * reference, csrc/fold.h:253-273). A row's source, final and boundary pages
+ * may coincide; pages of different rows must not (one row's stores are not
+ * ordered against another row's loads, as with the reference's kernels). */
 int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, const void *key_ref, const void *decay_ref,
                         const int64_t *state_addrs, const int64_t *state_block_strides, const int64_t *corr_addrs,
                         const int64_t *corr_block_strides, const int64_t *key_addrs,
@@ -149,7 +151,9 @@ int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, int64_t samp
  * Per-layer DEVICE tables: base addresses, block / dim / token strides
  * (elements). element_bytes is 2 or 4. `source` as in gdn_recoverssm_fold.
  * history is the kept history length, window the conv state's token extent
- * (history + Q - 1); every token read stays inside the window. */
+ * (history + Q - 1); every token read stays inside the window. Only the first
+ * `history` positions of the final (and boundary) slot change; slots of
+ * different rows must not coincide, as for gdn_recoverssm_fold. */
 int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int64_t *conv_block_strides,
                                 const int64_t *conv_dim_strides, const int64_t *conv_token_strides,
                                 const void *source, int32_t source_dtype, int64_t source_stride,

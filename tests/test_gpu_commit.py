@@ -180,6 +180,22 @@ def test_commit_dtypes(dev, state_dtype, key_dtype):
     _check_states(ckpts, want, state_dtype, set(plan["final"].tolist()) | set(plan["boundary"].tolist()))
 
 
+def _index_by_request(G, request_rows):
+    """The grouped plan reads the block table and positions by request index
+    (grouped_commit.py:147-187): lay them out so that plan row b's request owns
+    plan row b's pages. Rows never share a page, as in serving; the kernels,
+    like the reference's, do not order one row's stores against another row's
+    loads."""
+    if G["table"] is None:
+        return G
+    t, c = G["table"].clone(), G["C"].clone()
+    for b, r in enumerate(request_rows):
+        t[r] = G["table"][b]
+        c[r] = G["C"][b]
+    G["table"], G["C"] = t, c
+    return G
+
+
 def _entry(G, ctx, dev, request_rows):
     table = torch.zeros(G["B"], G["Q"], dtype=torch.int32, device=dev)
     table[:, 0] = G["src"].to(dev)
@@ -212,7 +228,8 @@ def test_grouped_bucket_two_groups_reordered_rows(dev, align):
     B = 6
     request_rows = [2, 0, 5, 1, 4, 3]
     sampled = torch.tensor([4, 0, 3, 1, 2, 4], dtype=torch.int32)
-    groups = [_group(B, 2, 4, 128, 128, 4, 2, align=align, seed=60 + g, page_offset=10 * g) for g in range(2)]
+    groups = [_index_by_request(_group(B, 2, 4, 128, 128, 4, 2, align=align, seed=60 + g, page_offset=10 * g),
+                                request_rows) for g in range(2)]
     # the accepted count is indexed by request; share it between groups
     contexts, entries, devs = [], [], []
     for G in groups:
@@ -280,6 +297,7 @@ def test_coordinator_seven_groups_three_buckets_and_publication(dev):
             for j in range(3):
                 table[r, int(src_col[r]) + j] = 1 + 3 * r + j
         G["table"], G["src"] = table, table[torch.arange(B), src_col].clone()
+        _index_by_request(G, request_rows)
         ckpts, convs, recs = _to_dev(G, dev)
         ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
         contexts.append(ctx)
