@@ -414,6 +414,45 @@ def main():
         torch.cuda.synchronize()
         kernel_ms["conv"] = sum(timer.elapsed(a, b) for a, b in ev) / reps
 
+    # The gated verify (gating and q/k L2 norm fused in) against the plain one,
+    # each over back-to-back launches on the same batch.
+    fused = None
+    if not args.kernel_only:
+        from gdn_recoverssm_ascend.kernels import gdn_recoverssm_verify_gated
+
+        gen = torch.Generator(device=dev).manual_seed(3)
+        a_raw = torch.randn(w.tokens, HV, generator=gen, device=dev)
+        b_raw = torch.randn(w.tokens, HV, generator=gen, device=dev)
+        A_log = torch.randn(HV, generator=gen, device=dev)
+        dt_bias = torch.randn(HV, generator=gen, device=dev)
+        rec32 = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=torch.float32)
+        gated_specs: list = []
+        gdn_recoverssm_verify_gated(a_raw, b_raw, inp.q, inp.k, inp.v, A_log=A_log, dt_bias=dt_bias,
+                                    checkpoint_state=w.checkpoints[0], replay_cache=rec32,
+                                    query_start_loc=m.query_start_loc, state_indices=m.state_indices,
+                                    spec_query_len=Q, out=out, _collect=gated_specs)
+
+        def alone(sp, reps=20):
+            for _ in range(3):
+                sp.launch()
+            e0, e1 = timer.event(), timer.event()
+            torch.cuda.synchronize()
+            timer.record(e0)
+            for _ in range(reps):
+                sp.launch()
+            timer.record(e1)
+            torch.cuda.synchronize()
+            return timer.elapsed(e0, e1) / reps
+
+        T_ = w.tokens
+        fused = {
+            "verify_us": round(alone(verify_specs[0]) * 1e3, 2),
+            "verify_gated_l2norm_us": round(alone(gated_specs[0]) * 1e3, 2),
+            "producer_round_trip_bytes": T_ * HV * (4 + 4) * 2 + T_ * H * K * 2 * 2 * 2,
+            "note": "gated verify reads raw a, b (fp32), q, k and writes FP32 key records; the producer "
+                    "round trip counts g/beta written and re-read and q/k normalised, written and re-read",
+        }
+
     nbytes = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
     total = nbytes["verify"] + nbytes["commit"]
     gbs = total / (step_ms * 1e-3) / 1e9
@@ -488,6 +527,7 @@ def main():
         "kernels": per_kernel,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "fused_gating": fused,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -13,10 +13,11 @@ static bool fits_i32(int64_t x) { return x >= INT32_MIN && x <= INT32_MAX; }
 
 using namespace gdn;
 
-extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v, const void *g, const void *beta,
-                                     const void *state, void *correction, void *key, void *decay, void *out,
-                                     const void *qsl, const void *indices, const int64_t *config,
-                                     int64_t config_len, float scale, const gdn_verify_ext *ext, void *stream) {
+static int verify_impl(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                       const void *state, void *correction, void *key, void *decay, void *out, const void *qsl,
+                       const void *indices, const int64_t *config, int64_t config_len, float scale,
+                       const gdn_verify_ext *ext, const void *a_log, const void *dt_bias,
+                       const gdn_gating_ext *gating, void *stream) {
   if (!config || config_len != GDN_VERIFY_CONFIG_FIELDS || !ext) {
     set_error("verify: tiling ABI expects %d config fields and an extension block", GDN_VERIFY_CONFIG_FIELDS);
     return GDN_ERR_INVALID;
@@ -71,8 +72,14 @@ extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v
     set_error("verify: activation token strides must be non-negative and span under 2 GiB per window");
     return GDN_ERR_UNSUPPORTED;
   }
+  if (gating && (!float_dt_ok(gating->a_log_dtype) || !float_dt_ok(gating->dt_bias_dtype) ||
+                 !(gating->softplus_beta > 0.0f))) {
+    set_error("verify: gating parameters need FP32/BF16/F16 A_log and dt_bias and a positive softplus beta");
+    return GDN_ERR_UNSUPPORTED;
+  }
   if (rows == 0 || tokens == 0) return GDN_OK;
-  if (!q || !k || !v || !g || !beta || !state || !correction || !key || !decay || !out || !qsl || !indices) {
+  if (!q || !k || !v || !g || !beta || !state || !correction || !key || !decay || !out || !qsl || !indices ||
+      (gating && (!a_log || !dt_bias))) {
     set_error("verify: null tensor pointer");
     return GDN_ERR_INVALID;
   }
@@ -127,6 +134,15 @@ extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v
   a.out_f32 = ext->out_dtype == GDN_DT_F32;
   a.l2norm = ext->qk_l2norm;
   a.key_per_value_head = ext->key_per_value_head;
+  if (gating) {
+    a.gated = 1;
+    a.a_log = a_log;
+    a.dt_bias = dt_bias;
+    a.a_log_dt = gating->a_log_dtype;
+    a.dt_bias_dt = gating->dt_bias_dtype;
+    a.softplus_beta = gating->softplus_beta;
+    a.softplus_threshold = gating->softplus_threshold;
+  }
   int j = 1;
   while (4 * E * j < K) j *= 2;
   const int qm = Q <= 1 ? 1 : Q <= 2 ? 2 : Q <= 4 ? 4 : 8;
@@ -148,4 +164,26 @@ extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v
     return GDN_ERR_LAUNCH;
   }
   return GDN_OK;
+}
+
+extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                                     const void *state, void *correction, void *key, void *decay, void *out,
+                                     const void *qsl, const void *indices, const int64_t *config,
+                                     int64_t config_len, float scale, const gdn_verify_ext *ext, void *stream) {
+  return verify_impl(q, k, v, g, beta, state, correction, key, decay, out, qsl, indices, config, config_len, scale,
+                     ext, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int gdn_recoverssm_verify_gated(const void *q, const void *k, const void *v, const void *a, const void *b,
+                                           const void *a_log, const void *dt_bias, const void *state,
+                                           void *correction, void *key, void *decay, void *out, const void *qsl,
+                                           const void *indices, const int64_t *config, int64_t config_len,
+                                           float scale, const gdn_verify_ext *ext, const gdn_gating_ext *gating,
+                                           void *stream) {
+  if (!gating) {
+    set_error("verify_gated: missing gating parameters");
+    return GDN_ERR_INVALID;
+  }
+  return verify_impl(q, k, v, a, b, state, correction, key, decay, out, qsl, indices, config, config_len, scale, ext,
+                     a_log, dt_bias, gating, stream);
 }

@@ -56,6 +56,10 @@ struct VerifyArgs {
   int32_t qsl_i64, idx_i64;                  // index dtypes: 1 for int64
   int32_t g_f32, beta_f32, key_f32, out_f32;  // 1: FP32, 0: activation dtype
   int32_t l2norm, key_per_value_head;
+  // Fused gating: g and beta hold the raw projections a and b.
+  const void *a_log, *dt_bias;
+  int32_t gated, a_log_dt, dt_bias_dt;
+  float softplus_beta, softplus_threshold;
 };
 
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
@@ -126,6 +130,16 @@ __device__ __forceinline__ void buf_ld4_act(__amdgpu_buffer_rsrc_t r, int byte_o
 // kernel never writes; the address is rounded down to a dword.
 __device__ __forceinline__ uint32_t scalar_word(uintptr_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(4))) uint32_t *>(addr & ~uintptr_t(3));
+}
+
+// One per-head parameter (FP32 or 16-bit) through the scalar cache.
+template <typename A>
+__device__ __forceinline__ float scalar_param(const void *p, int hv, int dt) {
+  if (dt == GDN_DT_F32) return __uint_as_float(scalar_word(reinterpret_cast<uintptr_t>(p) + uintptr_t(hv) * 4));
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(p) + uintptr_t(hv) * 2;
+  const uint32_t w = (scalar_word(addr) >> (int(addr & 2) * 8)) & 0xffffu;
+  if (dt == GDN_DT_BF16) return __uint_as_float(w << 16);
+  return float(__builtin_bit_cast(f16, uint16_t(w)));
 }
 
 template <typename S>
@@ -296,11 +310,24 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   __builtin_amdgcn_sched_barrier(0);  // keep block 0's loads ahead of block 1's
   load_block(1, bufB);
   float dec[QM], bet[QM];
+  float neg_a = 0.0f, dtb = 0.0f;
+  if (a.gated) {
+    neg_a = -expf(scalar_param<A>(a.a_log, hv, a.a_log_dt));
+    dtb = scalar_param<A>(a.dt_bias, hv, a.dt_bias_dt);
+  }
 #pragma unroll
   for (int t = 0; t < QM; ++t) {
     const bool tv = (valid_mask >> t) & 1u;
-    const float gv = a.g_f32 ? __uint_as_float(graw[t]) : bits_to_f32<A>((graw[t] >> gsh[t]) & 0xffffu);
-    const float bv = a.beta_f32 ? __uint_as_float(braw[t]) : bits_to_f32<A>((braw[t] >> bsh[t]) & 0xffffu);
+    float gv = a.g_f32 ? __uint_as_float(graw[t]) : bits_to_f32<A>((graw[t] >> gsh[t]) & 0xffffu);
+    float bv = a.beta_f32 ? __uint_as_float(braw[t]) : bits_to_f32<A>((braw[t] >> bsh[t]) & 0xffffu);
+    if (a.gated) {
+      // docs/reference/recoverssm_gdn_upstream.py:135-151
+      const float x = gv + dtb;
+      const float bx = a.softplus_beta * x;
+      const float sp = bx <= a.softplus_threshold ? log1pf(expf(bx)) / a.softplus_beta : x;
+      gv = neg_a * sp;
+      bv = 1.0f / (1.0f + expf(-bv));
+    }
     dec[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? expf(gv) : 1.0f)));
     bet[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? bv : 0.0f)));
   }

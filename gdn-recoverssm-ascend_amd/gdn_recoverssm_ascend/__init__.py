@@ -20,6 +20,7 @@ from .kernels import (  # noqa: F401
     ReplayRecordBuffers,
     counts,
     gdn_recoverssm_verify,
+    gdn_recoverssm_verify_gated,
     record_geometry_bytes,
     record_nbytes,
 )
@@ -42,6 +43,7 @@ __all__ = [
     "ReplayRecordBuffers",
     "counts",
     "gdn_recoverssm_verify",
+    "gdn_recoverssm_verify_gated",
     "initialize",
     "prepare_grouped_commit",
     "record_geometry_bytes",

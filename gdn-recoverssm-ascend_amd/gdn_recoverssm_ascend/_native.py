@@ -76,6 +76,15 @@ class FoldExt(ctypes.Structure):
     ]
 
 
+class GatingExt(ctypes.Structure):
+    _fields_ = [
+        ("a_log_dtype", c_i32),
+        ("dt_bias_dtype", c_i32),
+        ("softplus_beta", ctypes.c_float),
+        ("softplus_threshold", ctypes.c_float),
+    ]
+
+
 class PlanGroup(ctypes.Structure):
     _fields_ = [
         ("state_indices", c_vp), ("si_stride", c_i64), ("si_dtype", c_i32), ("pad0", c_i32),
@@ -120,6 +129,10 @@ def load() -> ctypes.CDLL:
         lib.gdn_recoverssm_last_error.argtypes = []
         lib.gdn_recoverssm_verify.restype = ctypes.c_int
         lib.gdn_recoverssm_verify.argtypes = [c_vp] * 12 + [P_i64, c_i64, ctypes.c_float, ctypes.POINTER(VerifyExt), c_vp]
+        lib.gdn_recoverssm_verify_gated.restype = ctypes.c_int
+        lib.gdn_recoverssm_verify_gated.argtypes = [c_vp] * 14 + [
+            P_i64, c_i64, ctypes.c_float, ctypes.POINTER(VerifyExt), ctypes.POINTER(GatingExt), c_vp,
+        ]
         lib.gdn_recoverssm_fold.restype = ctypes.c_int
         lib.gdn_recoverssm_fold.argtypes = [c_vp] * 18 + [P_i64, c_i64, ctypes.POINTER(FoldExt), c_vp]
         lib.gdn_recoverssm_plan.restype = ctypes.c_int
@@ -154,6 +167,7 @@ def exported_symbols() -> tuple[str, ...]:
         "gdn_recoverssm_abi_version",
         "gdn_recoverssm_last_error",
         "gdn_recoverssm_verify",
+        "gdn_recoverssm_verify_gated",
         "gdn_recoverssm_fold",
         "gdn_recoverssm_plan",
         "gdn_recoverssm_conv_compact",

@@ -242,13 +242,64 @@ def gdn_recoverssm_verify(
     [1, T, H, K]; v: [1, T, HV, V]; checkpoint_state: [blocks, HV, V, K];
     replay_cache: typed ``ReplayRecordBuffers`` or a packed FP32
     [rows, HV, spec_query_len, V + K + 1] tensor. Returns out [1, T, HV, V].
+    Reference: kernels.py:700-928.
     """
+    return _verify(g, beta, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
+                   query_start_loc=query_start_loc, state_indices=state_indices, spec_query_len=spec_query_len,
+                   scale=scale, qk_already_normalized=qk_already_normalized, out=out, gating=None, _collect=_collect)
+
+
+def gdn_recoverssm_verify_gated(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    checkpoint_state: torch.Tensor,
+    replay_cache: torch.Tensor | ReplayRecordBuffers,
+    query_start_loc: torch.Tensor,
+    state_indices: torch.Tensor,
+    spec_query_len: int,
+    scale: float | None = None,
+    qk_already_normalized: bool = False,
+    softplus_beta: float = 1.0,
+    softplus_threshold: float = 20.0,
+    out: torch.Tensor | None = None,
+    _collect: list | None = None,
+) -> torch.Tensor:
+    """Verify with the gating producer (and, by default, the q/k L2 norm)
+    fused in, as the gated verify of docs/reference/recoverssm_gdn_upstream.py:83-151.
+
+    ``a`` and ``b`` are the raw gate projections ([1, T, HV] or [T, HV]);
+    ``A_log`` and ``dt_bias`` are [HV]. Inside the kernel, in FP32:
+    g = -exp(A_log) * softplus(a + dt_bias) (softplus with ``softplus_beta``
+    and ``softplus_threshold``, as vLLM's fused_gdn_gating) and
+    beta = sigmoid(b). q and k are raw unless ``qk_already_normalized``. It
+    replaces the producers the layer runs before verify
+    (spec_forward.py:91-96) and their round trip through memory.
+    """
+    _require(A_log.ndim == 1 and dt_bias.ndim == 1, "A_log and dt_bias must be one-dimensional")
+    _require(A_log.stride(0) == 1 and dt_bias.stride(0) == 1, "A_log and dt_bias must be contiguous")
+    _require(float(softplus_beta) > 0.0, "softplus beta must be positive")
+    return _verify(a, b, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
+                   query_start_loc=query_start_loc, state_indices=state_indices, spec_query_len=spec_query_len,
+                   scale=scale, qk_already_normalized=qk_already_normalized, out=out,
+                   gating=(A_log, dt_bias, float(softplus_beta), float(softplus_threshold)), _collect=_collect)
+
+
+def _verify(g, beta, q, k, v, *, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
+            scale, qk_already_normalized, out, gating, _collect):
     _require(q.ndim == 4 and q.shape[0] == 1, "q must have shape [1, tokens, heads, dim]")
     _, total, H, K = q.shape
     _require(k.shape == q.shape, "q and k shapes differ")
     _require(v.ndim == 4 and tuple(v.shape[:2]) == (1, total), "v must have shape [1, tokens, value heads, dim]")
     HV, V = v.shape[-2], v.shape[-1]
     _require(H > 0 and HV >= H and HV % H == 0, "value heads must be a positive multiple of the q/k heads")
+    if gating is not None:
+        _require(gating[0].shape[0] == HV and gating[1].shape[0] == HV, "A_log and dt_bias need one entry per value head")
     _require(g.numel() == total * HV and beta.numel() == total * HV, "gate or beta shape is incompatible")
     g2 = g.reshape(total, HV)
     beta2 = beta.reshape(total, HV)
@@ -389,12 +440,7 @@ def gdn_recoverssm_verify(
     )
     cfg = N.i64_array(config)
     lib = _lib()
-    args = (
-        q.data_ptr(),
-        k.data_ptr(),
-        v.data_ptr(),
-        g2.data_ptr(),
-        beta2.data_ptr(),
+    tail = (
         checkpoint_state.data_ptr(),
         corr.data_ptr(),
         key_ptr,
@@ -407,13 +453,21 @@ def gdn_recoverssm_verify(
         float(scale),
         ctypes.byref(ext),
     )
-    spec = _LaunchSpec(
-        "verify",
-        lib.gdn_recoverssm_verify,
-        args,
-        _dev,
-        keepalive=(q, k, v, g2, beta2, checkpoint_state, corr, key_record, decay_record, out, query_start_loc, state_indices, cfg, ext),
-    )
+    keep = (q, k, v, g2, beta2, checkpoint_state, corr, key_record, decay_record, out, query_start_loc, state_indices,
+            cfg, ext)
+    if gating is None:
+        fn, args = lib.gdn_recoverssm_verify, (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(),
+                                                beta2.data_ptr()) + tail
+    else:
+        a_log, dt_bias, sp_beta, sp_threshold = gating
+        _require(all(t_.device == _dev for t_ in (a_log, dt_bias)), "inputs must be on the same device")
+        gext = N.GatingExt(a_log_dtype=N.dtype_code(a_log.dtype), dt_bias_dtype=N.dtype_code(dt_bias.dtype),
+                           softplus_beta=sp_beta, softplus_threshold=sp_threshold)
+        fn = lib.gdn_recoverssm_verify_gated
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(), beta2.data_ptr(), a_log.data_ptr(),
+                dt_bias.data_ptr()) + tail + (ctypes.byref(gext),)
+        keep = keep + (a_log, dt_bias, gext)
+    spec = _LaunchSpec("verify", fn, args, _dev, keepalive=keep)
     spec.config = tuple(int(x) for x in config)
     spec.scale = float(scale)
     if _collect is None:

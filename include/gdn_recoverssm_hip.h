@@ -19,6 +19,9 @@
  *                                   and kernels.py:1892-1928 (_prepare_commit_plan_kernel)
  *   gdn_recoverssm_conv_compact  -> grouped_commit.py:800-836, kernels.py:1931-1973
  *   gdn_recoverssm_publish       -> grouped_commit.py:531-610 (_publish_grouped_align_kernel)
+ *   gdn_recoverssm_verify_gated  -> the gated verify of docs/reference/recoverssm_gdn_upstream.py:83-151
+ *                                   (gating and q/k L2 norm fused into verify; the producers it
+ *                                   replaces are called at spec_forward.py:91-96)
  */
 #ifndef GDN_RECOVERSSM_HIP_H
 #define GDN_RECOVERSSM_HIP_H
@@ -96,6 +99,30 @@ int gdn_recoverssm_verify(const void *q, const void *k, const void *v, const voi
                           const void *state, void *correction, void *key, void *decay, void *out,
                           const void *qsl, const void *indices, const int64_t *config, int64_t config_len,
                           float scale, const gdn_verify_ext *ext, void *stream);
+
+/* Gating fused into verify (docs/reference/recoverssm_gdn_upstream.py:135-151):
+ * per token and value head, from the raw projections a and b,
+ *   g    = -exp(A_log[hv]) * softplus(a + dt_bias[hv]),
+ *   beta = sigmoid(b),
+ * with softplus(x) = log(1 + exp(sb*x)) / sb when sb*x <= threshold, else x
+ * (vLLM's fused_gdn_gating: sb = 1, threshold = 20), evaluated in FP32. */
+typedef struct gdn_gating_ext {
+  int32_t a_log_dtype;        /* A_log [HV]: F32 / BF16 / F16 */
+  int32_t dt_bias_dtype;      /* dt_bias [HV]: F32 / BF16 / F16 */
+  float softplus_beta;        /* > 0 */
+  float softplus_threshold;
+} gdn_gating_ext;
+
+/* Verify with the gating producer fused in: identical to gdn_recoverssm_verify
+ * except that `a` and `b` (token stride in config fields 11 and 12, dtypes in
+ * ext->g_dtype and ext->beta_dtype) are the raw gate projections and A_log /
+ * dt_bias are per-value-head parameters. Pair it with ext->qk_l2norm = 1 to
+ * fuse the q/k normalisation as well. The decay record holds exp(g). */
+int gdn_recoverssm_verify_gated(const void *q, const void *k, const void *v, const void *a, const void *b,
+                                const void *a_log, const void *dt_bias, const void *state, void *correction,
+                                void *key, void *decay, void *out, const void *qsl, const void *indices,
+                                const int64_t *config, int64_t config_len, float scale, const gdn_verify_ext *ext,
+                                const gdn_gating_ext *gating, void *stream);
 
 /* Grouped fold of the accepted prefix into every layer's checkpoint
  * (grouped_commit.py:377-480; csrc/fold.h:192-237). All table arguments are

@@ -17,6 +17,8 @@ Citations are ``file:line`` inside the reference plugin
 * ``oracle_fold``          -> kernels.py:1222-1324, grouped_commit.py:377-480
 * ``oracle_conv_compact``  -> kernels.py:1104-1169, grouped_commit.py:256-322
 * ``oracle_publish``       -> grouped_commit.py:531-560
+* ``oracle_gating``        -> docs/reference/recoverssm_gdn_upstream.py:135-151 (fused gating
+  of the gated verify; vLLM's ``fused_gdn_gating`` formula, called at spec_forward.py:91-93)
 
 How each part is pinned (see tests/test_oracle_*.py):
 
@@ -30,7 +32,10 @@ How each part is pinned (see tests/test_oracle_*.py):
   vectors of test_grouped_commit.py:173-292 / :626-637, plus a brute-force
   comparison against a per-token simulation of block ownership;
 * conv compaction: index identities against hand-built histories;
-* publish: the persistent-column vectors of test_grouped_commit.py:173-253.
+* publish: the persistent-column vectors of test_grouped_commit.py:173-253;
+* gating: torch's own ``softplus(x, beta, threshold)`` and ``sigmoid`` (library
+  routines with the same switch-over rule) and hand values (softplus(0) = ln 2,
+  the linear branch above the threshold).
 """
 
 from __future__ import annotations
@@ -575,6 +580,28 @@ def oracle_conv_compact(
             new[fin, :, :history] = fv
         out.append(new)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Fused gating (gated verify)
+# ---------------------------------------------------------------------------
+
+
+def oracle_gating(a, b, A_log, dt_bias, *, softplus_beta: float = 1.0, softplus_threshold: float = 20.0,
+                  dtype: torch.dtype = torch.float64):
+    """docs/reference/recoverssm_gdn_upstream.py:135-151 for every token and head.
+
+    a, b: [T, HV] raw gate projections; A_log, dt_bias: [HV]. Returns
+    (g, beta) with g = -exp(A_log) * softplus(a + dt_bias), where
+    softplus(x) = log(1 + exp(sb*x)) / sb if sb*x <= threshold else x, and
+    beta = sigmoid(b), in ``dtype``.
+    """
+    x = a.to(dtype) + dt_bias.to(dtype)[None, :]
+    bx = softplus_beta * x
+    sp = torch.where(bx <= softplus_threshold, torch.log(1 + torch.exp(bx)) / softplus_beta, x)
+    g = -torch.exp(A_log.to(dtype))[None, :] * sp
+    beta = 1 / (1 + torch.exp(-b.to(dtype)))
+    return g, beta
 
 
 # ---------------------------------------------------------------------------

@@ -87,6 +87,8 @@ int main(void) {
   printf("gdn_verify_ext %zu\n", sizeof(gdn_verify_ext));
   printf("gdn_fold_ext %zu\n", sizeof(gdn_fold_ext));
   printf("gdn_plan_group %zu\n", sizeof(gdn_plan_group));
+  printf("gdn_gating_ext %zu\n", sizeof(gdn_gating_ext));
+  F(gdn_gating_ext, softplus_beta) F(gdn_gating_ext, softplus_threshold)
   F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
   F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride)
   F(gdn_plan_group, block_table) F(gdn_plan_group, table_rows) F(gdn_plan_group, num_computed)
@@ -107,11 +109,13 @@ def test_ctypes_struct_layout_matches_c_compiler():
     assert int(got["gdn_verify_ext"]) == ctypes.sizeof(N.VerifyExt)
     assert int(got["gdn_fold_ext"]) == ctypes.sizeof(N.FoldExt)
     assert int(got["gdn_plan_group"]) == ctypes.sizeof(N.PlanGroup)
+    assert int(got["gdn_gating_ext"]) == ctypes.sizeof(N.GatingExt)
     for key, value in got.items():
         if "." not in key:
             continue
         struct, fld = key.split(".")
-        cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup}[struct]
+        cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup,
+               "gdn_gating_ext": N.GatingExt}[struct]
         assert getattr(cls, fld).offset == int(value), key
 
 

@@ -264,3 +264,46 @@ def test_verify_graph_replay(dev):
         torch.cuda.synchronize()
         for got, ref in zip((out, rec.correction, rec.key, rec.decay), want):
             assert torch.equal(got, ref), "graph replay differs from the eager launch"
+
+
+@pytest.mark.parametrize("ab_dtype,param_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                                  (torch.bfloat16, torch.bfloat16)])
+def test_gated_verify_fuses_gating_and_l2norm(dev, ab_dtype, param_dtype):
+    """gdn_recoverssm_verify_gated from raw a, b, q, k against the oracle fed
+    the oracle's own gating of the same raw inputs."""
+    from gdn_recoverssm_ascend.kernels import gdn_recoverssm_verify_gated
+
+    P = _problem(5, 2, 4, 128, 128, 4, qlens=[4, 3, 4, 0, 2], null_rows=(3,), normalise=False)
+    inp, B, H, HV, K, V, Q, T = P["inp"], P["B"], P["H"], P["HV"], P["K"], P["V"], P["Q"], P["T"]
+    gen = torch.Generator().manual_seed(21)
+    a = (torch.randn(T, HV, generator=gen) * 3).to(ab_dtype)
+    b = (torch.randn(T, HV, generator=gen) * 2).to(ab_dtype)
+    A_log = torch.randn(HV, generator=gen).to(param_dtype)
+    dt_bias = torch.randn(HV, generator=gen).to(param_dtype)
+    a[0, 0] = 30.0  # the linear branch of softplus
+    rec = ReplayRecordBuffers(
+        torch.full((B, HV, Q, V), SENT, device=dev), torch.full((B, H, Q, K), SENT, device=dev),
+        torch.full((B, HV, Q), SENT, device=dev),
+    )
+    out = torch.full((1, T, HV, V), SENT, dtype=torch.bfloat16, device=dev)
+    gdn_recoverssm_verify_gated(a.to(dev), b.to(dev), inp.q.to(dev), inp.k.to(dev), inp.v.to(dev),
+                                A_log=A_log.to(dev), dt_bias=dt_bias.to(dev), checkpoint_state=P["ckpt"].to(dev),
+                                replay_cache=rec, query_start_loc=P["qsl"].to(dev), state_indices=P["idx"].to(dev),
+                                spec_query_len=Q, out=out)
+    torch.cuda.synchronize()
+    g, beta = O.oracle_gating(a, b, A_log, dt_bias)
+    res = O.oracle_verify(inp.q, inp.k, inp.v, g, beta, P["ckpt"], P["qsl"], P["idx"], Q, qk_already_normalized=False)
+    w = res.out_written
+    got = out.cpu()[0]
+    assert torch.all(got[~w] == SENT)
+    assert_norm_close(got[w].double(), res.out[w], OUT_TOL, "gated out")
+    rw = res.record_written
+    corr = rec.correction.cpu()
+    m_c = rw[:, None, :, None].expand_as(corr)
+    assert_norm_close(corr[m_c].double(), res.correction[m_c], CORR_TOL, "gated correction")
+    decay = rec.decay.cpu()
+    m_d = rw[:, None, :].expand_as(decay)
+    torch.testing.assert_close(decay[m_d].double(), res.decay[m_d], rtol=3e-6, atol=0)
+    key = rec.key.cpu()
+    m_k = rw[:, None, :, None].expand_as(key)
+    torch.testing.assert_close(key[m_k].double(), res.key[m_k].double(), rtol=2e-6, atol=1e-7)

@@ -7,6 +7,7 @@ S_n = G_n S_0 + sum_t (G_n / G_t) c_t k_t^T.
 """
 
 import json
+import math
 import os
 
 import pytest
@@ -227,3 +228,24 @@ def test_fold_boundary_only_when_distinct_and_within_window():
     # a distinct valid boundary inside the window gets the snapshot after blen tokens
     out = _fold_one(ckpt, corr, key, dec, 2, final=2, boundary=3, blen=1)
     assert float(out[3]) == 20 * 0.5 + 1 and float(out[2]) == (20 * 0.5 + 1) * 0.5 + 1
+
+
+def test_gating_matches_library_softplus_and_sigmoid():
+    gen = torch.Generator().manual_seed(4)
+    a = torch.randn(37, 6, generator=gen, dtype=torch.float64) * 8
+    b = torch.randn(37, 6, generator=gen, dtype=torch.float64) * 4
+    A_log = torch.randn(6, generator=gen, dtype=torch.float64)
+    dt_bias = torch.randn(6, generator=gen, dtype=torch.float64)
+    for sb, thr in ((1.0, 20.0), (2.0, 5.0)):
+        g, beta = O.oracle_gating(a, b, A_log, dt_bias, softplus_beta=sb, softplus_threshold=thr)
+        want_g = -torch.exp(A_log)[None, :] * torch.nn.functional.softplus(a + dt_bias, beta=sb, threshold=thr)
+        torch.testing.assert_close(g, want_g, rtol=1e-13, atol=1e-13)
+        torch.testing.assert_close(beta, torch.sigmoid(b), rtol=1e-14, atol=1e-14)
+
+
+def test_gating_hand_values():
+    # softplus(0) = ln 2, beta(0) = 1/2; above the threshold softplus is the identity.
+    z = torch.zeros(1, 2, dtype=torch.float64)
+    g, beta = O.oracle_gating(z, z, torch.zeros(2, dtype=torch.float64), torch.tensor([0.0, 25.0], dtype=torch.float64))
+    assert abs(float(g[0, 0]) + math.log(2.0)) < 1e-15 and float(g[0, 1]) == -25.0
+    assert float(beta[0, 0]) == 0.5
