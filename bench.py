@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="align_b256")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--deferred", action="store_true",
+                    help="decode-loop workloads: fold each commit into the next step's verify")
     ap.add_argument("--loop-steps", type=int, default=None,
                     help="decode-loop workloads: speculative steps to time (default: the workload's own)")
     ap.add_argument("--kernel-only", action="store_true", help="skip the separate conv-compaction timing")
@@ -198,11 +200,17 @@ def decode_loop(args):
     """The decode-loop workload: every layer's verify, then one commit (plan,
     conv compaction, fold) across all layers, per speculative step, with the
     state carried from step to step (C += n, the source page becomes the final
-    page) and fresh accepted lengths each step."""
+    page) and fresh accepted lengths each step. With --deferred each step runs
+    the verify that applies the previous step's fold, then plan + conv."""
     import torch
 
     from gdn_recoverssm_ascend import workloads as W
-    from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+    from gdn_recoverssm_ascend.kernels import (
+        GDNRecoverSSMCommitContext,
+        ReplayRecordBuffers,
+        gdn_recoverssm_verify,
+        gdn_recoverssm_verify_deferred,
+    )
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -211,48 +219,84 @@ def decode_loop(args):
     L, B, Q, H, HV, K, V = s.layers, s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
     steps = s.steps if args.loop_steps is None else args.loop_steps
     m = w.meta
-    recs = [ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=w.inputs[0].k.dtype)
-            for _ in range(L)]
-    ctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, recs, spec_query_len=Q, max_num_reqs=B)
+    sets = 2 if args.deferred else 1
+    recs = [[ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=w.inputs[0].k.dtype)
+             for _ in range(L)] for _ in range(sets)]
+    ctxs = [GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, recs[i], spec_query_len=Q,
+                                                    max_num_reqs=B) for i in range(sets)]
     state_idx = m.state_indices.clone()
     computed = m.num_computed.clone()
     accepted = torch.zeros(B, dtype=torch.int32, device=dev)
     gen = torch.Generator().manual_seed(7)
     acc_all = torch.stack([W.sample_accepted(s, B, gen) for _ in range(steps + args.warmup)]).to(dev)
     outs = [torch.empty(1, w.tokens, HV, V, dtype=w.inputs[0].v.dtype, device=dev) for _ in range(L)]
-    verify_specs: list = []
-    for layer in range(L):
-        inp = w.inputs[layer]
-        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[layer],
-                              replay_cache=recs[layer], query_start_loc=m.query_start_loc, state_indices=state_idx,
-                              spec_query_len=Q, out=outs[layer], _collect=verify_specs)
-    commit_specs = ctx.make_commit_specs(accepted, state_idx, m.query_start_loc, block_table=m.block_table,
-                                         num_computed_tokens=computed, mamba_block_size=m.block_size, commit_conv=True)
-    lens, fin, bnd, blen = (ctx.commit_lens[:B], ctx.final_state_indices[:B], ctx.boundary_state_indices[:B],
-                            ctx.boundary_recovery_lens[:B])
+    commit_kw = dict(block_table=m.block_table, num_computed_tokens=computed, mamba_block_size=m.block_size,
+                     commit_conv=True)
+    cspecs, pendings = [], []
+    for i in range(sets):
+        specs_i: list = []
+        if args.deferred:
+            pendings.append(ctxs[i].commit_deferred(accepted, state_idx, m.query_start_loc, _collect=specs_i,
+                                                    **commit_kw))
+        else:
+            specs_i = list(ctxs[i].make_commit_specs(accepted, state_idx, m.query_start_loc, **commit_kw))
+        cspecs.append(specs_i)
+    vspecs = []
+    for i in range(sets):
+        specs_i = []
+        for layer in range(L):
+            inp = w.inputs[layer]
+            kw = dict(checkpoint_state=w.checkpoints[layer], replay_cache=recs[i][layer],
+                      query_start_loc=m.query_start_loc, state_indices=state_idx, spec_query_len=Q, out=outs[layer],
+                      _collect=specs_i)
+            if args.deferred:
+                gdn_recoverssm_verify_deferred(inp.g, inp.beta, inp.q, inp.k, inp.v,
+                                               pending=pendings[1 - i][layer], **kw)
+            else:
+                gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, **kw)
+        vspecs.append(specs_i)
     hist_lens = torch.empty(steps, 4, B, dtype=torch.int32, device=dev)
 
-    def step(i, record=None):
-        accepted.copy_(acc_all[i])
-        for sp in verify_specs:
-            sp.launch()
-        for sp in commit_specs:
-            sp.launch()
-        if record is not None:
-            for j, t in enumerate((lens, fin, bnd, blen)):
-                hist_lens[record, j].copy_(t)
-        committed = lens > 0
-        computed.add_(lens.to(computed.dtype))
-        state_idx.copy_(torch.where(committed, fin.to(state_idx.dtype), state_idx))
+    def plan_of(i):
+        c = ctxs[i % sets]
+        return c.commit_lens[:B], c.final_state_indices[:B], c.boundary_state_indices[:B], c.boundary_recovery_lens[:B]
 
+    def carry(i):
+        lens_, fin_ = plan_of(i)[:2]
+        computed.add_(lens_.to(computed.dtype))
+        state_idx.copy_(torch.where(lens_ > 0, fin_.to(state_idx.dtype), state_idx))
+
+    def step(i, record=None, marks=None):
+        accepted.copy_(acc_all[i])
+        if marks:
+            timer.record(marks[0])
+        for sp in vspecs[i % sets]:
+            sp.launch()
+        if marks:
+            timer.record(marks[1])
+        for sp in cspecs[i % sets]:
+            sp.launch()
+        if marks:
+            timer.record(marks[2])
+        if record is not None:
+            for j, t in enumerate(plan_of(i)):
+                hist_lens[record, j].copy_(t)
+        carry(i)
+
+    def restart():
+        state_idx.copy_(start_idx)
+        computed.copy_(start_c)
+        for c in ctxs:
+            c.commit_lens.zero_()  # no pending commit for the first deferred verify
+
+    stream = torch.cuda.current_stream(dev)
+    timer = _HipTimer(stream.cuda_stream)
     start_idx, start_c = state_idx.clone(), computed.clone()
+    restart()
     for i in range(args.warmup):
         step(steps + i)
     torch.cuda.synchronize()
-    state_idx.copy_(start_idx)
-    computed.copy_(start_c)
-    stream = torch.cuda.current_stream(dev)
-    timer = _HipTimer(stream.cuda_stream)
+    restart()
     t0, t1 = timer.event(), timer.event()
     torch.cuda.synchronize()
     timer.record(t0)
@@ -263,26 +307,15 @@ def decode_loop(args):
     total_ms = timer.elapsed(t0, t1)
 
     # Per-phase split over a second pass of the same steps (state restarted).
-    state_idx.copy_(start_idx)
-    computed.copy_(start_c)
+    restart()
     ev = [(timer.event(), timer.event(), timer.event()) for _ in range(steps)]
     torch.cuda.synchronize()
     for i in range(steps):
-        a, b, c = ev[i]
-        accepted.copy_(acc_all[i])
-        timer.record(a)
-        for sp in verify_specs:
-            sp.launch()
-        timer.record(b)
-        for sp in commit_specs:
-            sp.launch()
-        timer.record(c)
-        committed = lens > 0
-        computed.add_(lens.to(computed.dtype))
-        state_idx.copy_(torch.where(committed, fin.to(state_idx.dtype), state_idx))
+        step(i, marks=ev[i])
     torch.cuda.synchronize()
     verify_ms = sum(timer.elapsed(a, b) for a, b, _ in ev) / steps
     commit_ms = sum(timer.elapsed(b, c) for _, b, c in ev) / steps
+    lens, fin, bnd, blen = plan_of(0)
 
     nb = byte_model(w, lens, fin, bnd, blen)  # verify part is the same every step
     verify_b = nb["verify"] * L
@@ -299,8 +332,10 @@ def decode_loop(args):
     step_ms = total_ms / steps
     total_b = verify_b * steps + commit_b + conv_b
     gbs = total_b / (total_ms * 1e-3) / 1e9
+    mode = "deferred commit (fold applied by the next verify)" if args.deferred else "verify then commit"
     line = {
-        "metric": f"decode loop: {L} GDN layers verify + one grouped commit per step, B={B} Q={Q}, state carried",
+        "metric": f"decode loop: {L} GDN layers verify + one grouped commit per step, B={B} Q={Q}, state carried"
+                  + (", deferred commit" if args.deferred else ""),
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -319,7 +354,15 @@ def decode_loop(args):
         "phases_us_per_step": {"verify_all_layers": round(verify_ms * 1e3, 1), "commit": round(commit_ms * 1e3, 1)},
         "bytes_per_step": {"verify": verify_b, "commit": round(commit_b / steps), "conv": round(conv_b / steps)},
         "tokens_committed_per_step": round(tokens_committed / steps, 1),
+        "mode": mode,
     }
+    if args.deferred:
+        # The step's state reads that the deferred commit removes: one page read
+        # per committed (row, layer).
+        saved = sum(int((hist_lens[i, 0] > 0).sum()) for i in range(steps)) * L * HV * V * K * 4
+        line["hbm_bytes_per_step"] = round((total_b - saved) / steps)
+        line["hbm_gbs"] = round((total_b - saved) / (total_ms * 1e-3) / 1e9, 1)
+        line["note"] = "value divides the ordinary flow's algorithmic bytes by this loop's time"
     print(json.dumps(line), flush=True)
     return 0
 
@@ -455,6 +498,65 @@ def main():
 
     nbytes = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
     total = nbytes["verify"] + nbytes["commit"]
+
+    # The deferred commit: each step runs the verify that also applies the
+    # previous step's fold, then the plan (the fold is left to the next step).
+    # Two record sets alternate; the same batch repeats, as in the main region.
+    deferred = None
+    if not args.kernel_only:
+        from gdn_recoverssm_ascend.kernels import gdn_recoverssm_verify_deferred
+
+        recs2 = [rec, ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype)]
+        ctx2 = [ctx, GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, [recs2[1]],
+                                                            spec_query_len=Q, max_num_reqs=B)]
+        commit_kw = dict(block_table=m.block_table if align else None,
+                         num_computed_tokens=m.num_computed if align else None,
+                         mamba_block_size=m.block_size if align else None, commit_conv=False)
+        pend = [None, None]
+        dspecs = [[], []]
+        for i in range(2):
+            specs_i: list = []
+            pend[i] = ctx2[i].commit_deferred(m.accepted, m.state_indices, m.query_start_loc, _collect=specs_i,
+                                              **commit_kw)
+            dspecs[i] = specs_i
+        vdef = [[], []]
+        for i in range(2):
+            gdn_recoverssm_verify_deferred(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0],
+                                           replay_cache=recs2[i], pending=pend[1 - i][0],
+                                           query_start_loc=m.query_start_loc, state_indices=m.state_indices,
+                                           spec_query_len=Q, out=out, _collect=vdef[i])
+
+        def dstep(i):
+            vdef[i][0].launch()  # applies the fold planned in the other context
+            for sp in dspecs[i]:
+                sp.launch()
+
+        for sp in dspecs[1]:
+            sp.launch()  # a plan for the first deferred verify to apply
+        for i in range(args.warmup):
+            dstep(i % 2)
+        torch.cuda.synchronize()
+        d0, d1 = timer.event(), timer.event()
+        timer.record(d0)
+        for i in range(args.steps):
+            dstep(i % 2)
+        timer.record(d1)
+        torch.cuda.synchronize()
+        dms = timer.elapsed(d0, d1) / args.steps
+        # HBM bytes of a deferred step: verify's, plus the fold's writes and
+        # record reads; the fold's read of the state is the one removed.
+        s_bytes = HV * V * K * 4
+        fold_read_state = nbytes["active_rows"] * s_bytes
+        actual = nbytes["verify"] + nbytes["commit"] - fold_read_state
+        deferred = {
+            "us_per_step": round(dms * 1e3, 2),
+            "equivalent_gbs": round(total / (dms * 1e-3) / 1e9, 1),
+            "equivalent_frac": round(total / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_bytes_per_step": actual,
+            "hbm_gbs": round(actual / (dms * 1e-3) / 1e9, 1),
+            "note": "verify_deferred (applies the previous step's fold) + plan per step; equivalent_gbs divides the "
+                    "ordinary step's algorithmic bytes by this step time",
+        }
     gbs = total / (step_ms * 1e-3) / 1e9
 
     per_kernel = {}
@@ -528,6 +630,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fused_gating": fused,
+        "deferred_commit": deferred,
     }
     print(json.dumps(line), flush=True)
     return 0

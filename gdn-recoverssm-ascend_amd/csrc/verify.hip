@@ -17,7 +17,7 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
                        const void *state, void *correction, void *key, void *decay, void *out, const void *qsl,
                        const void *indices, const int64_t *config, int64_t config_len, float scale,
                        const gdn_verify_ext *ext, const void *a_log, const void *dt_bias,
-                       const gdn_gating_ext *gating, void *stream) {
+                       const gdn_gating_ext *gating, const gdn_pending_commit *pending, void *stream) {
   if (!config || config_len != GDN_VERIFY_CONFIG_FIELDS || !ext) {
     set_error("verify: tiling ABI expects %d config fields and an extension block", GDN_VERIFY_CONFIG_FIELDS);
     return GDN_ERR_INVALID;
@@ -77,8 +77,25 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     set_error("verify: gating parameters need FP32/BF16/F16 A_log and dt_bias and a positive softplus beta");
     return GDN_ERR_UNSUPPORTED;
   }
-  if (rows == 0 || tokens == 0) return GDN_OK;
-  if (!q || !k || !v || !g || !beta || !state || !correction || !key || !decay || !out || !qsl || !indices ||
+  if (pending) {
+    const bool ok = ext->state_dtype == GDN_DT_F32 && pending->record_rows > 0 &&
+                    act_or_f32(pending->key_dtype) && fits_i32(pending->corr_strides[1]) &&
+                    fits_i32(pending->corr_strides[2]) && fits_i32(pending->key_strides[1]) &&
+                    fits_i32(pending->key_strides[2]) && fits_i32(pending->decay_strides[1]) &&
+                    fits_i32(pending->decay_strides[2]) &&
+                    (Q - 1) * pending->corr_strides[2] + V < int64_t(kWindowBytes) / 4 &&
+                    (Q - 1) * pending->key_strides[2] + K < int64_t(kWindowBytes) / 4;
+    if (!ok) {
+      set_error("verify_deferred: FP32 state, FP32 or activation-typed pending keys and 32-bit record strides "
+                "are required");
+      return GDN_ERR_UNSUPPORTED;
+    }
+  }
+  // With nothing to verify, only pending commits give the launch work.
+  if (rows == 0 || (tokens == 0 && !pending)) return GDN_OK;
+  const bool need_window = tokens > 0;
+  if (!state || !qsl || !indices ||
+      (need_window && (!q || !k || !v || !g || !beta || !correction || !key || !decay || !out)) ||
       (gating && (!a_log || !dt_bias))) {
     set_error("verify: null tensor pointer");
     return GDN_ERR_INVALID;
@@ -134,6 +151,39 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   a.out_f32 = ext->out_dtype == GDN_DT_F32;
   a.l2norm = ext->qk_l2norm;
   a.key_per_value_head = ext->key_per_value_head;
+  if (pending) {
+    if (!pending->rows || !pending->source || !pending->lengths || !pending->final_indices ||
+        !pending->boundary_indices || !pending->boundary_lengths || !pending->correction || !pending->key ||
+        !pending->decay) {
+      set_error("verify_deferred: null pending-commit pointer");
+      return GDN_ERR_INVALID;
+    }
+    if (pending->correction == correction || pending->key == key || pending->decay == decay) {
+      set_error("verify_deferred: the pending commit's records are the buffers this verify writes");
+      return GDN_ERR_INVALID;
+    }
+    a.p_rows = pending->rows;
+    a.p_src = pending->source;
+    a.p_len = pending->lengths;
+    a.p_final = pending->final_indices;
+    a.p_bnd = pending->boundary_indices;
+    a.p_blen = pending->boundary_lengths;
+    a.p_corr = static_cast<const float *>(pending->correction);
+    a.p_key = pending->key;
+    a.p_decay = static_cast<const float *>(pending->decay);
+    a.p_corr_rs = pending->corr_strides[0];
+    a.p_corr_hs = int32_t(pending->corr_strides[1]);
+    a.p_corr_ts = int32_t(pending->corr_strides[2]);
+    a.p_key_rs = pending->key_strides[0];
+    a.p_key_hs = int32_t(pending->key_strides[1]);
+    a.p_key_ts = int32_t(pending->key_strides[2]);
+    a.p_decay_rs = pending->decay_strides[0];
+    a.p_decay_hs = int32_t(pending->decay_strides[1]);
+    a.p_decay_ts = int32_t(pending->decay_strides[2]);
+    a.p_key_f32 = pending->key_dtype == GDN_DT_F32;
+    a.p_key_per_value_head = pending->key_per_value_head;
+    a.p_record_rows = int32_t(pending->record_rows > 0x7fffffff ? 0x7fffffff : pending->record_rows);
+  }
   if (gating) {
     a.gated = 1;
     a.a_log = a_log;
@@ -154,9 +204,9 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   auto s = static_cast<hipStream_t>(stream);
   const dim3 gd(static_cast<unsigned>(a.NVT * value_heads), static_cast<unsigned>(rows), 1u);
   switch (ext->state_dtype) {
-    case GDN_DT_BF16: launch_verify_state<bf16>(act, j, qm, gd, s, a); break;
-    case GDN_DT_F16: launch_verify_state<f16>(act, j, qm, gd, s, a); break;
-    default: launch_verify_state<float>(act, j, qm, gd, s, a); break;
+    case GDN_DT_BF16: launch_verify_state<bf16>(act, j, qm, pending != nullptr, gd, s, a); break;
+    case GDN_DT_F16: launch_verify_state<f16>(act, j, qm, pending != nullptr, gd, s, a); break;
+    default: launch_verify_state<float>(act, j, qm, pending != nullptr, gd, s, a); break;
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
@@ -171,7 +221,21 @@ extern "C" int gdn_recoverssm_verify(const void *q, const void *k, const void *v
                                      const void *qsl, const void *indices, const int64_t *config,
                                      int64_t config_len, float scale, const gdn_verify_ext *ext, void *stream) {
   return verify_impl(q, k, v, g, beta, state, correction, key, decay, out, qsl, indices, config, config_len, scale,
-                     ext, nullptr, nullptr, nullptr, stream);
+                     ext, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int gdn_recoverssm_verify_deferred(const void *q, const void *k, const void *v, const void *g,
+                                              const void *beta, const void *state, void *correction, void *key,
+                                              void *decay, void *out, const void *qsl, const void *indices,
+                                              const int64_t *config, int64_t config_len, float scale,
+                                              const gdn_verify_ext *ext, const gdn_pending_commit *pending,
+                                              void *stream) {
+  if (!pending) {
+    set_error("verify_deferred: missing pending commit");
+    return GDN_ERR_INVALID;
+  }
+  return verify_impl(q, k, v, g, beta, state, correction, key, decay, out, qsl, indices, config, config_len, scale,
+                     ext, nullptr, nullptr, nullptr, pending, stream);
 }
 
 extern "C" int gdn_recoverssm_verify_gated(const void *q, const void *k, const void *v, const void *a, const void *b,
@@ -185,5 +249,5 @@ extern "C" int gdn_recoverssm_verify_gated(const void *q, const void *k, const v
     return GDN_ERR_INVALID;
   }
   return verify_impl(q, k, v, a, b, state, correction, key, decay, out, qsl, indices, config, config_len, scale, ext,
-                     a_log, dt_bias, gating, stream);
+                     a_log, dt_bias, gating, nullptr, stream);
 }

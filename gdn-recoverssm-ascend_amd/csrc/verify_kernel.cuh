@@ -60,6 +60,14 @@ struct VerifyArgs {
   const void *a_log, *dt_bias;
   int32_t gated, a_log_dt, dt_bias_dt;
   float softplus_beta, softplus_threshold;
+  // Deferred commit (kernels instantiated with DEFER): the previous step's
+  // plan row for every current row and that step's records.
+  const int32_t *p_rows, *p_src, *p_len, *p_final, *p_bnd, *p_blen;
+  const float *p_corr, *p_decay;
+  const void *p_key;
+  int64_t p_corr_rs, p_key_rs, p_decay_rs;
+  int32_t p_corr_hs, p_corr_ts, p_key_hs, p_key_ts, p_decay_hs, p_decay_ts;
+  int32_t p_key_f32, p_key_per_value_head, p_record_rows;
 };
 
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
@@ -173,7 +181,14 @@ __device__ __forceinline__ int64_t ld_idx(const void *p, int64_t i, bool i64) {
   return i64 ? static_cast<const int64_t *>(p)[i] : int64_t(static_cast<const int32_t *>(p)[i]);
 }
 
-template <typename S, typename A, int J, int QM>
+// DEFER: before verifying, apply the previous step's commit for this row (the
+// fold of kernels.py:1222-1324, folded into the next verify): the state comes
+// from the pending commit's source page, its accepted prefix is replayed from
+// the previous step's records block by block, the result is stored to the
+// final page (and the boundary snapshot to the boundary page), and the window
+// is verified from the folded values. Each state page is read once per step
+// instead of twice. FP32 state only.
+template <typename S, typename A, int J, int QM, bool DEFER>
 __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   constexpr int E = Chunk<S>::E;       // elements per 16-byte chunk
   constexpr int KP = 4 * E * J;        // K padded to 4 k-slots x J chunks x E
@@ -184,6 +199,8 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   __shared__ float gram_lds[QM][NV];
   __shared__ float d_lds[64][NV + 1];  // GEMV results of one 64-row half tile
   __shared__ float inv_lds[NV];
+  __shared__ __align__(16) float pk_lds[DEFER ? QM : 1][DEFER ? KP : 1];  // pending commit's keys
+  static_assert(!DEFER || sizeof(S) == 4, "the deferred commit is built for FP32 state");
 
   const int nvt = a.NVT;
   const int hv = int(blockIdx.x) / nvt;
@@ -202,7 +219,25 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const int64_t slot = ld_idx(a.indices, int64_t(b) * a.idx_s, a.idx_i64);
   const int64_t out_base = int64_t(hv) * V + row0;
 
-  if (slot <= a.null_block || slot >= a.blocks) {
+  // Pending commit of the previous step (same validity rule as the fold,
+  // kernels.py:1232-1242 / csrc/fold.h:192-205).
+  bool pend = false, pstore_b = false;
+  int pn = 0, pblen = 0, prow = 0;
+  int64_t psrc = 0, pfin = 0, pbnd = 0;
+  if constexpr (DEFER) {
+    prow = int(ld_idx(a.p_rows, b, false));
+    pn = int(ld_idx(a.p_len, b, false));
+    psrc = ld_idx(a.p_src, b, false);
+    pfin = ld_idx(a.p_final, b, false);
+    pbnd = ld_idx(a.p_bnd, b, false);
+    pblen = int(ld_idx(a.p_blen, b, false));
+    pend = prow >= 0 && prow < a.p_record_rows && pn > 0 && pn <= Q && psrc > a.null_block && psrc < a.blocks &&
+           pfin > a.null_block && pfin < a.blocks;
+    pstore_b = pend && pbnd > a.null_block && pbnd < a.blocks && pbnd != pfin && pblen > 0 && pblen <= pn;
+  }
+  const int pend_len = pend ? pn : 0;  // tokens of the pending commit to replay
+  const bool null_slot = slot <= a.null_block || slot >= a.blocks;
+  if (null_slot) {
     // Null or out-of-range page: zero outputs for the window, records untouched
     // (kernels.py:569-583).
     for (int t = 0; t < Q; ++t) {
@@ -211,7 +246,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       for (int r = lane; r < kTileRows; r += kVerifyThreads)
         if (row0 + r < V) st_f32_or<A>(a.out, tok * a.out_ts + out_base + r, a.out_f32 != 0, 0.0f);
     }
-    return;
+    if (!pend) return;
   }
   // Token validity is uniform across the wave (kernels.py:612).
   uint32_t valid_mask = 0;
@@ -220,7 +255,12 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     const int64_t tok = bos + t;
     if (t < Q && t < qlen && tok >= 0 && tok < a.tokens) valid_mask |= 1u << t;
   }
-  if (valid_mask == 0) return;
+  if (valid_mask == 0 && !pend) return;
+  // A pending commit on a row with nothing to verify still has to be applied:
+  // that wave runs the whole pipeline with no token (every input load reads
+  // out of range and nothing but the folded tile is stored).
+  const bool verify_row = !null_slot && valid_mask != 0;
+  if (!verify_row) valid_mask = 0;
 
   const int li = lane & 15, ls = lane >> 4;  // MFMA row / column index and k-slot
 
@@ -228,6 +268,30 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   constexpr int C4 = KP / 4;  // 4-element chunks per vector
   constexpr int STAGE_PASSES = (NV * C4 + kVerifyThreads - 1) / kVerifyThreads;
   constexpr int AS = int(sizeof(A));
+  // DEFER: the pending commit's keys (token t, element kk) for LDS, FP32 or
+  // activation-typed records (one of the two loads reads out of range).
+  constexpr int PK_PASSES = DEFER ? (QM * C4 + kVerifyThreads - 1) / kVerifyThreads : 1;
+  float pkx[PK_PASSES][4];
+  if constexpr (DEFER) {
+    const int key_head = a.p_key_per_value_head ? hv : h;
+    const int64_t kbase = int64_t(prow) * a.p_key_rs + int64_t(key_head) * a.p_key_hs;
+    const bool kf32 = a.p_key_f32 != 0;
+    const __amdgpu_buffer_rsrc_t rpk = make_rsrc(a.p_key, kbase * (kf32 ? 4 : AS));
+    int lim = pend_len;
+    asm volatile("" : "+v"(lim));  // per-lane select, not a branch (see load_block)
+#pragma unroll
+    for (int p = 0; p < PK_PASSES; ++p) {
+      const int idx = p * kVerifyThreads + lane;
+      const int t = idx / C4, kk = (idx - t * C4) * 4;
+      const bool live = t < lim && kk < K;
+      const int el = t * a.p_key_ts + kk;
+      float x32[4], xa[4];
+      buf_ld4_act<float>(rpk, live && kf32 ? el * 4 : kOutOfRange, x32);
+      buf_ld4_act<A>(rpk, live && !kf32 ? el * AS : kOutOfRange, xa);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pkx[p][e] = x32[e] + xa[e];
+    }
+  }
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, bos * a.q_ts * AS), rk = make_rsrc(a.k, bos * a.k_ts * AS);
   float xs[STAGE_PASSES][4];
 #pragma unroll
@@ -287,28 +351,51 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   // per chunk and the block step in soffset. Rows >= V lie past the resource's
   // extent and read as zero; chunks >= K get an out-of-range offset.
   // Rows of block rb: rb*16 + li; the lane loads chunks 4j + ls of its row.
-  const S *sp = static_cast<const S *>(a.state) + slot * a.state_bs + int64_t(hv) * a.state_hs +
-                int64_t(row0) * a.state_vs;
   const int tile_rows = V - row0 < kTileRows ? V - row0 : kTileRows;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<S *>(sp), 0, tile_rows * a.state_vs * int(sizeof(S)), 0x00020000);
+  const int tile_bytes = tile_rows * a.state_vs * int(sizeof(S));
+  auto tile_rsrc = [&](int64_t page, bool use) {
+    const S *tp = static_cast<const S *>(a.state) + page * a.state_bs + int64_t(hv) * a.state_hs +
+                  int64_t(row0) * a.state_vs;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(use ? tp : static_cast<const S *>(a.state)), 0,
+                                             use ? tile_bytes : 0, 0x00020000);
+  };
+  // DEFER with a pending commit: read the pending source page; the folded
+  // tile goes to the final page (and its snapshot to the boundary page).
+  const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(pend ? psrc : slot, true);
+  const __amdgpu_buffer_rsrc_t rfin = tile_rsrc(pfin, pend);
+  const __amdgpu_buffer_rsrc_t rbnd = tile_rsrc(pbnd, pstore_b);
   const int row_bytes = a.state_vs * int(sizeof(S));
   const int lane_off = li * row_bytes + ls * 16;
+  // The pending corrections of the lane's row, fetched with each block.
+  const __amdgpu_buffer_rsrc_t rpc =
+      make_rsrc(a.p_corr, (int64_t(prow) * a.p_corr_rs + int64_t(hv) * a.p_corr_hs + row0) * 4);
   // One form for every K, and every block is loaded (blocks past V read as
   // zero): a conditional load would leave a path on which it was not issued,
   // and the wait counts of every later MFMA would have to assume that path,
   // draining the pipeline at each block.
-  auto load_block = [&](int rb, uint4 (&dst)[J]) {
+  auto load_block = [&](int rb, uint4 (&dst)[J], float (&pc)[QM]) {
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
       dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
     }
+    if constexpr (DEFER) {
+      const int v = rb * 16 + li;
+      // Tokens to replay as a per-lane value: a select on it stays a select
+      // (a wave-uniform bound would turn each load into a branch).
+      int lim = row0 + v < V ? pend_len : 0;
+      asm volatile("" : "+v"(lim));
+#pragma unroll
+      for (int t = 0; t < QM; ++t)
+        pc[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rpc, t < lim ? (t * a.p_corr_ts + v) * 4 : kOutOfRange, 0, 0));
+    }
   };
   uint4 bufA[J], bufB[J];
-  load_block(0, bufA);
+  float pcA[QM], pcB[QM];
+  load_block(0, bufA, pcA);
   __builtin_amdgcn_sched_barrier(0);  // keep block 0's loads ahead of block 1's
-  load_block(1, bufB);
+  load_block(1, bufB, pcB);
   float dec[QM], bet[QM];
   float neg_a = 0.0f, dtb = 0.0f;
   if (a.gated) {
@@ -361,7 +448,68 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     if (lane < QM && ((valid_mask >> lane) & 1u))
       a.decay[int64_t(b) * a.decay_rs + int64_t(hv) * a.decay_hs + int64_t(lane) * a.decay_ts] = dl;
   }
+  // DEFER: the pending keys to LDS, the pending decays to scalars.
+  float pdec[QM];
+  if constexpr (DEFER) {
+#pragma unroll
+    for (int p = 0; p < PK_PASSES; ++p) {
+      const int idx = p * kVerifyThreads + lane;
+      const int t = idx / C4, kk = (idx - t * C4) * 4;
+      if (t < QM) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pk_lds[t][kk + e] = pkx[p][e];
+      }
+    }
+    const uintptr_t dbase = reinterpret_cast<uintptr_t>(a.p_decay);
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const bool live = pend && t < pn;
+      const uintptr_t off =
+          live ? uintptr_t((int64_t(prow) * a.p_decay_rs + int64_t(hv) * a.p_decay_hs + int64_t(t) * a.p_decay_ts) * 4)
+               : 0;
+      pdec[t] = live ? __uint_as_float(scalar_word(dbase + off)) : 1.0f;
+    }
+  }
   wave_lds_sync();
+
+  // DEFER: replay the pending accepted prefix on one block in registers,
+  // h <- fma(c_t, k_t, h * d_t) as the fold does, storing the boundary snapshot
+  // after `boundary_len` tokens and the final state after n (kernels.py:1242-1324).
+  // Both stores are issued on every path (an unused one reads as out of range)
+  // so the wait counts of the loads in flight never depend on the row.
+  auto fold_block = [&](int rb, uint4 (&buf)[J], const float (&pc)[QM]) {
+    if constexpr (DEFER) {
+      const int seg = pstore_b ? pblen : 0;
+      auto apply = [&](int lo, int hi) {
+#pragma unroll
+        for (int t = 0; t < QM; ++t) {
+          if (t >= lo && t < hi) {
+            const float d = pdec[t], c = pc[t];
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+              const float4 kv = *reinterpret_cast<const float4 *>(&pk_lds[t][E * (4 * j + ls)]);
+              buf[j].x = __float_as_uint(__builtin_fmaf(c, kv.x, __uint_as_float(buf[j].x) * d));
+              buf[j].y = __float_as_uint(__builtin_fmaf(c, kv.y, __uint_as_float(buf[j].y) * d));
+              buf[j].z = __float_as_uint(__builtin_fmaf(c, kv.z, __uint_as_float(buf[j].z) * d));
+              buf[j].w = __float_as_uint(__builtin_fmaf(c, kv.w, __uint_as_float(buf[j].w) * d));
+            }
+          }
+        }
+      };
+      auto store = [&](__amdgpu_buffer_rsrc_t r) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, buf[j]),
+                                                 r, vo, rb * 16 * row_bytes, 0);
+        }
+      };
+      apply(0, seg);
+      store(rbnd);
+      apply(seg, pn);
+      store(rfin);
+    }
+  };
 
   if (a.l2norm) {
     // kernels.py:645-648: x * rsqrt(sum(x*x) + 1e-6) for q and k, then q *= scale.
@@ -463,10 +611,12 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   };
 #pragma unroll
   for (int rb = 0; rb < NRB; rb += 2) {
+    fold_block(rb, bufA, pcA);
     gemv_block(rb, bufA);
-    if (rb + 2 < NRB) load_block(rb + 2, bufA);
+    if (rb + 2 < NRB) load_block(rb + 2, bufA, pcA);
+    fold_block(rb + 1, bufB, pcB);
     gemv_block(rb + 1, bufB);
-    if (rb + 3 < NRB) load_block(rb + 3, bufB);
+    if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
     if (rb + 2 == NRB / 2) load_v(1);
     if ((rb + 2) % 4 == 0 && row0 + (rb - 2) * 16 < V) recurrence((rb + 2) / 4 - 1);
   }
@@ -474,40 +624,53 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 
 // Launch for one state type; defined per state type in verify_<state>.hip.
 template <typename S>
-void launch_verify_state(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a);
+void launch_verify_state(int act_dt, int j, int qm, bool deferred, dim3 grid, hipStream_t s, const VerifyArgs &a);
 
-template <typename S, typename A, int J>
+template <typename S, typename A, int J, bool DEFER>
 static void launch_verify_q(int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
   switch (qm) {
-    case 1: hipLaunchKernelGGL((verify_kernel<S, A, J, 1>), grid, dim3(kVerifyThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((verify_kernel<S, A, J, 2>), grid, dim3(kVerifyThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((verify_kernel<S, A, J, 4>), grid, dim3(kVerifyThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL((verify_kernel<S, A, J, 8>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((verify_kernel<S, A, J, 1, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((verify_kernel<S, A, J, 2, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((verify_kernel<S, A, J, 4, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((verify_kernel<S, A, J, 8, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
   }
 }
 
 // J: 16-byte chunks per lane per row, KP = 4 * E * J <= 256, so J <= 16 for
-// f32 state and J <= 8 for 16-bit state.
-template <typename S, typename A>
+// f32 state and J <= 8 for 16-bit state. The deferred-commit kernels exist for
+// FP32 state only (the host rejects other state types).
+template <typename S, typename A, bool DEFER>
 static void launch_verify_j(int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
   switch (j) {
-    case 1: launch_verify_q<S, A, 1>(qm, grid, s, a); break;
-    case 2: launch_verify_q<S, A, 2>(qm, grid, s, a); break;
-    case 4: launch_verify_q<S, A, 4>(qm, grid, s, a); break;
-    case 8: launch_verify_q<S, A, 8>(qm, grid, s, a); break;
+    case 1: launch_verify_q<S, A, 1, DEFER>(qm, grid, s, a); break;
+    case 2: launch_verify_q<S, A, 2, DEFER>(qm, grid, s, a); break;
+    case 4: launch_verify_q<S, A, 4, DEFER>(qm, grid, s, a); break;
+    case 8: launch_verify_q<S, A, 8, DEFER>(qm, grid, s, a); break;
     default:
-      if constexpr (Chunk<S>::E == 4) launch_verify_q<S, A, 16>(qm, grid, s, a);
+      if constexpr (Chunk<S>::E == 4) launch_verify_q<S, A, 16, DEFER>(qm, grid, s, a);
       break;
   }
 }
 
+template <typename S, typename A>
+static void launch_verify_d(bool deferred, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
+  if constexpr (sizeof(S) == 4) {
+    if (deferred) {
+      launch_verify_j<S, A, true>(j, qm, grid, s, a);
+      return;
+    }
+  }
+  launch_verify_j<S, A, false>(j, qm, grid, s, a);
+}
+
 #define GDN_DEFINE_VERIFY_LAUNCH(STATE)                                                                   \
   template <>                                                                                             \
-  void launch_verify_state<STATE>(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) { \
+  void launch_verify_state<STATE>(int act_dt, int j, int qm, bool deferred, dim3 grid, hipStream_t s,    \
+                                  const VerifyArgs &a) {                                                  \
     switch (act_dt) {                                                                                     \
-      case GDN_DT_BF16: launch_verify_j<STATE, bf16>(j, qm, grid, s, a); break;                           \
-      case GDN_DT_F16: launch_verify_j<STATE, f16>(j, qm, grid, s, a); break;                             \
-      default: launch_verify_j<STATE, float>(j, qm, grid, s, a); break;                                   \
+      case GDN_DT_BF16: launch_verify_d<STATE, bf16>(deferred, j, qm, grid, s, a); break;                 \
+      case GDN_DT_F16: launch_verify_d<STATE, f16>(deferred, j, qm, grid, s, a); break;                   \
+      default: launch_verify_d<STATE, float>(deferred, j, qm, grid, s, a); break;                         \
     }                                                                                                     \
   }
 

@@ -17,9 +17,11 @@ from .kernels import (  # noqa: F401
     MAX_SPEC_QUERY_LEN,
     NULL_BLOCK_ID,
     GDNRecoverSSMCommitContext,
+    PendingCommit,
     ReplayRecordBuffers,
     counts,
     gdn_recoverssm_verify,
+    gdn_recoverssm_verify_deferred,
     gdn_recoverssm_verify_gated,
     record_geometry_bytes,
     record_nbytes,
@@ -40,9 +42,11 @@ __all__ = [
     "GroupedCommitCoordinator",
     "MAX_SPEC_QUERY_LEN",
     "NULL_BLOCK_ID",
+    "PendingCommit",
     "ReplayRecordBuffers",
     "counts",
     "gdn_recoverssm_verify",
+    "gdn_recoverssm_verify_deferred",
     "gdn_recoverssm_verify_gated",
     "initialize",
     "prepare_grouped_commit",

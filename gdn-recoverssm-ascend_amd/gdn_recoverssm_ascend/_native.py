@@ -85,6 +85,17 @@ class GatingExt(ctypes.Structure):
     ]
 
 
+class PendingCommit(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_vp), ("source", c_vp), ("lengths", c_vp), ("final_indices", c_vp),
+        ("boundary_indices", c_vp), ("boundary_lengths", c_vp),
+        ("correction", c_vp), ("key", c_vp), ("decay", c_vp),
+        ("record_rows", c_i64),
+        ("corr_strides", c_i64 * 3), ("key_strides", c_i64 * 3), ("decay_strides", c_i64 * 3),
+        ("key_dtype", c_i32), ("key_per_value_head", c_i32),
+    ]
+
+
 class PlanGroup(ctypes.Structure):
     _fields_ = [
         ("state_indices", c_vp), ("si_stride", c_i64), ("si_dtype", c_i32), ("pad0", c_i32),
@@ -133,6 +144,10 @@ def load() -> ctypes.CDLL:
         lib.gdn_recoverssm_verify_gated.argtypes = [c_vp] * 14 + [
             P_i64, c_i64, ctypes.c_float, ctypes.POINTER(VerifyExt), ctypes.POINTER(GatingExt), c_vp,
         ]
+        lib.gdn_recoverssm_verify_deferred.restype = ctypes.c_int
+        lib.gdn_recoverssm_verify_deferred.argtypes = [c_vp] * 12 + [
+            P_i64, c_i64, ctypes.c_float, ctypes.POINTER(VerifyExt), ctypes.POINTER(PendingCommit), c_vp,
+        ]
         lib.gdn_recoverssm_fold.restype = ctypes.c_int
         lib.gdn_recoverssm_fold.argtypes = [c_vp] * 18 + [P_i64, c_i64, ctypes.POINTER(FoldExt), c_vp]
         lib.gdn_recoverssm_plan.restype = ctypes.c_int
@@ -168,6 +183,7 @@ def exported_symbols() -> tuple[str, ...]:
         "gdn_recoverssm_last_error",
         "gdn_recoverssm_verify",
         "gdn_recoverssm_verify_gated",
+        "gdn_recoverssm_verify_deferred",
         "gdn_recoverssm_fold",
         "gdn_recoverssm_plan",
         "gdn_recoverssm_conv_compact",

@@ -290,8 +290,91 @@ def gdn_recoverssm_verify_gated(
                    gating=(A_log, dt_bias, float(softplus_beta), float(softplus_threshold)), _collect=_collect)
 
 
+@dataclass
+class PendingCommit:
+    """One layer's commit left for the next verify (``gdn_recoverssm_verify_deferred``).
+
+    Plan arrays are int32 and indexed by the NEXT step's row: ``rows`` is the
+    record row of the pending commit (-1: none), then source page, accepted
+    length, final page, boundary page and boundary length of that commit.
+    ``records`` are the typed records the pending step's verify wrote; the next
+    verify must write a different record buffer.
+    """
+
+    rows: torch.Tensor
+    source: torch.Tensor
+    lengths: torch.Tensor
+    final: torch.Tensor
+    boundary: torch.Tensor
+    boundary_len: torch.Tensor
+    records: "ReplayRecordBuffers"
+
+
+def gdn_recoverssm_verify_deferred(
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    checkpoint_state: torch.Tensor,
+    replay_cache: "ReplayRecordBuffers",
+    pending: PendingCommit,
+    query_start_loc: torch.Tensor,
+    state_indices: torch.Tensor,
+    spec_query_len: int,
+    scale: float | None = None,
+    qk_already_normalized: bool = True,
+    out: torch.Tensor | None = None,
+    _collect: list | None = None,
+) -> torch.Tensor:
+    """Verify with the previous step's commit folded in (the deferred commit of
+    docs/GDN-RecoverSSM-实现方案.md:515-527; FP32 state, typed records).
+
+    For each row with a pending commit the kernel reads the pending source page,
+    replays its accepted prefix exactly as the fold does (kernels.py:1222-1324),
+    stores the result to the final page (and the boundary snapshot), and
+    verifies this step's window from the folded state, so every page is read
+    once per step. Rows without a pending commit verify from
+    ``state_indices`` as ``gdn_recoverssm_verify`` does.
+    """
+    rec = pending.records
+    _require(isinstance(rec, ReplayRecordBuffers), "the deferred commit needs typed record buffers")
+    _require(isinstance(replay_cache, ReplayRecordBuffers), "the deferred commit needs typed record buffers")
+    _require(
+        rec.correction.data_ptr() != replay_cache.correction.data_ptr(),
+        "the pending commit's records must not be the records this verify writes",
+    )
+    _require(checkpoint_state.dtype == torch.float32, "the deferred commit is built for FP32 state")
+    batch = state_indices.shape[0]
+    arrays = (pending.rows, pending.source, pending.lengths, pending.final, pending.boundary, pending.boundary_len)
+    _require(
+        all(t_.dtype == torch.int32 and t_.ndim == 1 and t_.shape[0] >= batch and t_.stride(0) == 1 for t_ in arrays),
+        "pending plan arrays must be contiguous int32 covering every row",
+    )
+    _require(
+        rec.correction.shape[1:] == replay_cache.correction.shape[1:] and rec.key.shape[1:] == replay_cache.key.shape[1:],
+        "pending records do not match this layer's record geometry",
+    )
+    pc = N.PendingCommit(
+        rows=arrays[0].data_ptr(), source=arrays[1].data_ptr(), lengths=arrays[2].data_ptr(),
+        final_indices=arrays[3].data_ptr(), boundary_indices=arrays[4].data_ptr(),
+        boundary_lengths=arrays[5].data_ptr(), correction=rec.correction.data_ptr(), key=rec.key.data_ptr(),
+        decay=rec.decay.data_ptr(), record_rows=rec.correction.shape[0],
+        key_dtype=N.dtype_code(rec.key.dtype), key_per_value_head=0,
+    )
+    for i in range(3):
+        pc.corr_strides[i] = rec.correction.stride(i)
+        pc.key_strides[i] = rec.key.stride(i)
+        pc.decay_strides[i] = rec.decay.stride(i)
+    return _verify(g, beta, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
+                   query_start_loc=query_start_loc, state_indices=state_indices, spec_query_len=spec_query_len,
+                   scale=scale, qk_already_normalized=qk_already_normalized, out=out, gating=None,
+                   pending=(pc, arrays, rec), _collect=_collect)
+
+
 def _verify(g, beta, q, k, v, *, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
-            scale, qk_already_normalized, out, gating, _collect):
+            scale, qk_already_normalized, out, gating, _collect, pending=None):
     _require(q.ndim == 4 and q.shape[0] == 1, "q must have shape [1, tokens, heads, dim]")
     _, total, H, K = q.shape
     _require(k.shape == q.shape, "q and k shapes differ")
@@ -361,7 +444,7 @@ def _verify(g, beta, q, k, v, *, checkpoint_state, replay_cache, query_start_loc
         out = torch.empty(1, total, HV, V, dtype=v.dtype, device=v.device)
     _require(tuple(out.shape) == (1, total, HV, V) and out.stride()[2:] == (V, 1), "output shape or layout is incompatible")
     batch = state_indices.shape[0]
-    if total == 0 or batch == 0:
+    if batch == 0 or (total == 0 and pending is None):
         return out
     # What the gfx950 kernels are built for (checked before any launch).
     _require(q.dtype == k.dtype == v.dtype, "q, k and v must share one activation dtype")
@@ -455,7 +538,12 @@ def _verify(g, beta, q, k, v, *, checkpoint_state, replay_cache, query_start_loc
     )
     keep = (q, k, v, g2, beta2, checkpoint_state, corr, key_record, decay_record, out, query_start_loc, state_indices,
             cfg, ext)
-    if gating is None:
+    if pending is not None:
+        pc, arrays, rec = pending
+        fn = lib.gdn_recoverssm_verify_deferred
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(), beta2.data_ptr()) + tail + (ctypes.byref(pc),)
+        keep = keep + (pc, arrays, rec)
+    elif gating is None:
         fn, args = lib.gdn_recoverssm_verify, (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(),
                                                 beta2.data_ptr()) + tail
     else:
@@ -640,6 +728,8 @@ class GDNRecoverSSMCommitContext:
         context.record_bytes = sum(record_nbytes(r) for r in replays)
         context.align_valid = z()
         context.align_col = z()
+        context.plan_source = z()  # canonical source page of each planned row (NULL when invalid)
+        context.pending_rows = torch.arange(max_num_reqs, dtype=torch.int32, device=dev)
         return context
 
     @classmethod
@@ -813,6 +903,7 @@ class GDNRecoverSSMCommitContext:
         mamba_block_size: int | None = None,
         commit_conv: bool = True,
         _collect: list | None = None,
+        _fold_source: torch.Tensor | None = None,
     ) -> None:
         """Fold accepted GDN and convolution inputs into every layer's checkpoint."""
         batch = state_indices.shape[0]
@@ -881,7 +972,7 @@ class GDNRecoverSSMCommitContext:
             num_accepted_tokens.shape[0],
             grp,
             1,
-            None,
+            self.plan_source.data_ptr(),
             self.commit_lens.data_ptr(),
             self.final_state_indices.data_ptr(),
             self.boundary_state_indices.data_ptr(),
@@ -957,7 +1048,7 @@ class GDNRecoverSSMCommitContext:
                 self.key_base_addrs, self.key_block_strides, self.decay_base_addrs, self.decay_block_strides,
             ),
             layer_groups=None,
-            source=state_indices,
+            source=state_indices if _fold_source is None else _fold_source,
             plan=(self.commit_lens, self.final_state_indices, self.boundary_state_indices, self.boundary_recovery_lens),
             refs=(rr, kr, dr),
         )
@@ -968,6 +1059,50 @@ class GDNRecoverSSMCommitContext:
             for spec in specs:
                 spec.launch()
         self._last_specs = tuple(specs)
+
+    def commit_deferred(
+        self,
+        num_accepted_tokens: torch.Tensor,
+        state_indices: torch.Tensor,
+        query_start_loc: torch.Tensor,
+        request_indices: torch.Tensor | None = None,
+        block_table: torch.Tensor | None = None,
+        num_computed_tokens: torch.Tensor | None = None,
+        mamba_block_size: int | None = None,
+        commit_conv: bool = True,
+        _collect: list | None = None,
+    ) -> tuple:
+        """Plan the commit (and compact the conv states) but leave the fold to
+        the next step's ``gdn_recoverssm_verify_deferred``; returns one
+        ``PendingCommit`` per layer. ``flush_deferred`` applies the pending
+        fold directly instead (for a step that runs no verify)."""
+        _require(self.record_layout == "soa", "the deferred commit needs typed record buffers")
+        specs: list = []
+        self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices=request_indices,
+                    block_table=block_table, num_computed_tokens=num_computed_tokens,
+                    mamba_block_size=mamba_block_size, commit_conv=commit_conv, _collect=specs,
+                    _fold_source=self.plan_source)
+        self._deferred_fold = next(sp for sp in specs if sp.name == "fold")
+        now = [sp for sp in specs if sp.name != "fold"]
+        if _collect is not None:
+            _collect.extend(now)
+        else:
+            for sp in now:
+                sp.launch()
+        return tuple(
+            PendingCommit(self.pending_rows, self.plan_source, self.commit_lens, self.final_state_indices,
+                          self.boundary_state_indices, self.boundary_recovery_lens, rec)
+            for rec in self.records
+        )
+
+    def flush_deferred(self, _collect: list | None = None) -> None:
+        """Apply the last ``commit_deferred`` plan with the ordinary fold."""
+        spec = getattr(self, "_deferred_fold", None)
+        _require(spec is not None, "no deferred commit to flush")
+        if _collect is not None:
+            _collect.append(spec)
+        else:
+            spec.launch()
 
 
 def _make_fold_spec(

@@ -22,6 +22,9 @@
  *   gdn_recoverssm_verify_gated  -> the gated verify of docs/reference/recoverssm_gdn_upstream.py:83-151
  *                                   (gating and q/k L2 norm fused into verify; the producers it
  *                                   replaces are called at spec_forward.py:91-96)
+ *   gdn_recoverssm_verify_deferred -> the "deferred commit" of docs/GDN-RecoverSSM-实现方案.md:515-527,
+ *                                   563-568: the fold (csrc/ops.cpp:170-239) applied inside the
+ *                                   next step's verify
  */
 #ifndef GDN_RECOVERSSM_HIP_H
 #define GDN_RECOVERSSM_HIP_H
@@ -123,6 +126,46 @@ int gdn_recoverssm_verify_gated(const void *q, const void *k, const void *v, con
                                 void *key, void *decay, void *out, const void *qsl, const void *indices,
                                 const int64_t *config, int64_t config_len, float scale, const gdn_verify_ext *ext,
                                 const gdn_gating_ext *gating, void *stream);
+
+/* The previous step's commit of one layer, left for the next verify to apply.
+ * Plan arrays (DEVICE, int32, indexed by the CURRENT step's row): `rows` gives
+ * the record row of the pending commit (-1: none), the rest are the plan
+ * outputs of that commit (source, accepted length, final, boundary, boundary
+ * length; see gdn_recoverssm_plan). The records are the previous step's typed
+ * SoA planes (or packed FP32 rows, key_per_value_head = 1); they must not be
+ * the buffers the current verify writes. Strides in elements. */
+typedef struct gdn_pending_commit {
+  const int32_t *rows;
+  const int32_t *source;
+  const int32_t *lengths;
+  const int32_t *final_indices;
+  const int32_t *boundary_indices;
+  const int32_t *boundary_lengths;
+  const void *correction;     /* [R', HV, Q, V] FP32 */
+  const void *key;            /* [R', H, Q, K] FP32 or the activation dtype */
+  const void *decay;          /* [R', HV, Q] FP32 */
+  int64_t record_rows;        /* R' */
+  int64_t corr_strides[3];    /* row, head, token */
+  int64_t key_strides[3];
+  int64_t decay_strides[3];
+  int32_t key_dtype;
+  int32_t key_per_value_head;
+} gdn_pending_commit;
+
+/* Verify with the previous step's commit folded in (FP32 state only; no
+ * counterpart entry in the reference, whose design notes propose it). For
+ * every row with a pending commit, the wave reads the pending source page,
+ * replays the accepted prefix exactly as gdn_recoverssm_fold does, stores the
+ * result to the final page (and the boundary snapshot), and verifies the
+ * current window from the folded state; state_indices is not read for such a
+ * row (it is expected to name the pending final page). Rows without a pending
+ * commit verify from state_indices as gdn_recoverssm_verify does. A pending
+ * commit must appear under some current row, and rows must not share pages. */
+int gdn_recoverssm_verify_deferred(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                                   const void *state, void *correction, void *key, void *decay, void *out,
+                                   const void *qsl, const void *indices, const int64_t *config,
+                                   int64_t config_len, float scale, const gdn_verify_ext *ext,
+                                   const gdn_pending_commit *pending, void *stream);
 
 /* Grouped fold of the accepted prefix into every layer's checkpoint
  * (grouped_commit.py:377-480; csrc/fold.h:192-237). All table arguments are

@@ -88,6 +88,8 @@ int main(void) {
   printf("gdn_fold_ext %zu\n", sizeof(gdn_fold_ext));
   printf("gdn_plan_group %zu\n", sizeof(gdn_plan_group));
   printf("gdn_gating_ext %zu\n", sizeof(gdn_gating_ext));
+  printf("gdn_pending_commit %zu\n", sizeof(gdn_pending_commit));
+  F(gdn_pending_commit, record_rows) F(gdn_pending_commit, decay_strides) F(gdn_pending_commit, key_per_value_head)
   F(gdn_gating_ext, softplus_beta) F(gdn_gating_ext, softplus_threshold)
   F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
   F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride)
@@ -110,12 +112,13 @@ def test_ctypes_struct_layout_matches_c_compiler():
     assert int(got["gdn_fold_ext"]) == ctypes.sizeof(N.FoldExt)
     assert int(got["gdn_plan_group"]) == ctypes.sizeof(N.PlanGroup)
     assert int(got["gdn_gating_ext"]) == ctypes.sizeof(N.GatingExt)
+    assert int(got["gdn_pending_commit"]) == ctypes.sizeof(N.PendingCommit)
     for key, value in got.items():
         if "." not in key:
             continue
         struct, fld = key.split(".")
         cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup,
-               "gdn_gating_ext": N.GatingExt}[struct]
+               "gdn_gating_ext": N.GatingExt, "gdn_pending_commit": N.PendingCommit}[struct]
         assert getattr(cls, fld).offset == int(value), key
 
 
