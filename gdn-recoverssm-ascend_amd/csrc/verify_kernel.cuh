@@ -652,14 +652,13 @@ static void launch_verify_j(int j, int qm, dim3 grid, hipStream_t s, const Verif
   }
 }
 
+// The deferred-commit kernels (FP32 state) live in their own translation unit
+// (verify_f32_deferred.hip) so the two halves compile in parallel.
+void launch_verify_f32_deferred(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a);
+
 template <typename S, typename A>
 static void launch_verify_d(bool deferred, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
-  if constexpr (sizeof(S) == 4) {
-    if (deferred) {
-      launch_verify_j<S, A, true>(j, qm, grid, s, a);
-      return;
-    }
-  }
+  (void)deferred;
   launch_verify_j<S, A, false>(j, qm, grid, s, a);
 }
 
@@ -667,6 +666,10 @@ static void launch_verify_d(bool deferred, int j, int qm, dim3 grid, hipStream_t
   template <>                                                                                             \
   void launch_verify_state<STATE>(int act_dt, int j, int qm, bool deferred, dim3 grid, hipStream_t s,    \
                                   const VerifyArgs &a) {                                                  \
+    if (deferred) {                                                                                       \
+      launch_verify_f32_deferred(act_dt, j, qm, grid, s, a);                                              \
+      return;                                                                                             \
+    }                                                                                                     \
     switch (act_dt) {                                                                                     \
       case GDN_DT_BF16: launch_verify_d<STATE, bf16>(deferred, j, qm, grid, s, a); break;                 \
       case GDN_DT_F16: launch_verify_d<STATE, f16>(deferred, j, qm, grid, s, a); break;                   \

@@ -68,34 +68,36 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False, jobs: int = 4) -> str:
-    """Compile every source (in parallel) and link the shared library."""
+def build(verbose: bool = False, jobs: int = min(6, os.cpu_count() or 1)) -> str:
+    """Compile every source (in parallel, largest first) and link the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(LIB_DIR, exist_ok=True)
     cc = hipcc()
-    srcs = sources()
+    srcs = sorted(sources(), key=os.path.getsize, reverse=True)
+    srcs = sorted(srcs, key=lambda p: 0 if os.path.basename(p).startswith("verify_") else 1)
     with tempfile.TemporaryDirectory(prefix="gdn_build_") as tmp:
-        objs = []
-        procs = []
-        for src in srcs:
+
+        def compile_one(src):
             obj = os.path.join(tmp, os.path.basename(src) + ".o")
-            objs.append(obj)
             cmd = [cc, *compile_flags(), "-c", src, "-o", obj]
             if verbose:
                 print(" ".join(cmd), flush=True)
-            procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
-            if len([p for _, p in procs if p.poll() is None]) >= jobs:
-                procs[0][1].wait()
-        errors = []
-        for src, p in procs:
-            out, _ = p.communicate()
-            text = out.decode(errors="replace")
+            r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+            text = r.stdout.decode(errors="replace")
             text = "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l and l.strip() != "1 warning generated.")
-            if p.returncode != 0:
-                errors.append(f"{src}:\n{text}")
-            elif verbose and text.strip():
-                print(text)
+            return src, obj, r.returncode, text
+
+        with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+            results = list(pool.map(compile_one, srcs))
+        errors = [f"{src}:\n{text}" for src, _, rc, text in results if rc != 0]
+        if verbose:
+            for src, _, rc, text in results:
+                if rc == 0 and text.strip():
+                    print(text)
         if errors:
             raise RuntimeError("hipcc failed:\n" + "\n".join(errors))
+        objs = [obj for _, obj, _, _ in results]
         tmp_lib = LIB_PATH + ".tmp"
         link = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib]
         r = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
