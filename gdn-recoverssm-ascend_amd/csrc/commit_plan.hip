@@ -6,99 +6,14 @@
 // (single context). Every index derived from data is bounds-checked against the
 // sizes the host passes; an out-of-range index makes the row a no-op (the
 // reference would read outside the tensor there).
-#include "gdn_common.cuh"
+#include "plan_row.cuh"
 
 namespace gdn {
-
-struct PlanArgs {
-  const void *sampled;
-  int64_t sampled_stride, sampled_len;
-  int32_t sampled_dtype, num_groups;
-  gdn_plan_group groups[GDN_PLAN_MAX_GROUPS];
-  int32_t *source, *lens, *final_, *boundary, *boundary_lens, *valid, *col;
-  const void *idx_mapping;
-  int64_t idx_len;
-  int32_t idx_dtype;
-  uint32_t flags;
-  int32_t *pcols, *pacc;
-  int64_t plen, rows, cap, null_block, Q;
-};
-
-// Division with truncation toward zero, as the reference kernels' integer `//`.
-__device__ __forceinline__ int64_t tdiv(int64_t a, int64_t b) { return a / b; }
 
 __global__ __launch_bounds__(64) void plan_kernel(PlanArgs a) {
   const int64_t row = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (row >= a.rows) return;
-  const bool align = (a.flags & GDN_PLAN_ALIGN) != 0;
-  const bool grouped = (a.flags & GDN_PLAN_GROUPED) != 0;
-  const int64_t null_block = a.null_block;
-  bool all_valid = true;
-  int64_t shared_col = -1, shared_request = -1;
-  for (int gi = 0; gi < a.num_groups; ++gi) {
-    const gdn_plan_group &g = a.groups[gi];
-    const int64_t request = g.request_indices ? load_index(g.request_indices, row * g.map_stride, g.map_dtype) : row;
-    const int64_t source = load_index(g.state_indices, row * g.si_stride, g.si_dtype);
-    const int64_t bos = load_index(g.query_start_loc, row * g.qsl_stride, g.qsl_dtype);
-    const int64_t eos = load_index(g.query_start_loc, (row + 1) * g.qsl_stride, g.qsl_dtype);
-    const int64_t qlen = eos - bos;
-    bool request_ok = request >= 0 && request < a.sampled_len;
-    if (align) request_ok = request_ok && request < g.table_rows && request < g.computed_len;
-    const int64_t accepted =
-        request_ok ? int64_t(int32_t(load_index(a.sampled, request * a.sampled_stride, a.sampled_dtype))) : 0;
-    int64_t count = min(max(accepted, int64_t(0)), qlen);
-    count = min(count, a.Q);
-    int64_t final_idx = source, boundary = null_block, blen = 0, col = 0;
-    bool computed_ok = true;
-    if (align && request_ok) {
-      const int64_t C =
-          int64_t(int32_t(load_index(g.num_computed, request * g.computed_stride, g.computed_dtype)));
-      computed_ok = C >= 0;
-      const int64_t position = C + count;
-      col = min(tdiv(max(position - 1, int64_t(0)), g.block_size), g.table_width - 1);
-      final_idx = load_index(g.block_table, request * g.table_row_stride + col * g.table_col_stride, g.table_dtype);
-      const int64_t next_boundary = (tdiv(C, g.block_size) + 1) * g.block_size;
-      const bool crossed = position >= next_boundary;
-      blen = next_boundary - C;
-      const int64_t bcol = tdiv(next_boundary, g.block_size) - 1;
-      bool load_b = crossed && bcol >= 0 && bcol < g.table_width;
-      if (grouped) load_b = load_b && computed_ok;
-      boundary = load_b ? load_index(g.block_table, request * g.table_row_stride + bcol * g.table_col_stride,
-                                     g.table_dtype)
-                        : null_block;
-    }
-    const bool geometry = bos >= 0 && bos <= eos && qlen <= a.Q;
-    const bool valid = request_ok && geometry && source > null_block && source < g.num_blocks &&
-                       final_idx > null_block && final_idx < g.num_blocks && count > 0 && count <= qlen &&
-                       computed_ok;
-    const bool boundary_ok = boundary > null_block && boundary < g.num_blocks;
-    if (align && !boundary_ok) blen = 0;
-    if (grouped && !boundary_ok) boundary = null_block;
-    const int64_t off = int64_t(gi) * a.cap + row;
-    if (a.source) a.source[off] = int32_t(valid ? source : null_block);
-    a.lens[off] = int32_t(valid ? count : 0);
-    a.final_[off] = int32_t(valid ? final_idx : null_block);
-    a.boundary[off] = int32_t(valid ? boundary : null_block);
-    a.boundary_lens[off] = int32_t(valid ? blen : 0);
-    if (a.valid) a.valid[off] = valid ? 1 : 0;
-    if (a.col) a.col[off] = int32_t(col);
-    if (gi == 0) {
-      shared_col = col;
-      shared_request = request;
-    } else {
-      all_valid = all_valid && col == shared_col && request == shared_request;
-    }
-    all_valid = all_valid && valid;
-  }
-  if ((a.flags & GDN_PLAN_PUBLISH) && align) {
-    if (shared_request >= 0 && shared_request < a.idx_len) {
-      const int64_t slot = load_index(a.idx_mapping, shared_request, a.idx_dtype);
-      if (all_valid && slot >= 0 && slot < a.plen) {
-        a.pcols[slot] = int32_t(shared_col);
-        a.pacc[slot] = 1;
-      }
-    }
-  }
+  plan_write_row(a, row);
 }
 
 // Conv-state compaction. One workgroup per (layer, row, tile of
@@ -244,50 +159,49 @@ static bool index_dtype_ok(int32_t dt) { return dt == GDN_DT_I32 || dt == GDN_DT
 
 using namespace gdn;
 
-extern "C" int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, int64_t sampled_stride,
-                                   int64_t sampled_len, const gdn_plan_group *groups, int32_t num_groups,
-                                   int32_t *source_plan, int32_t *lens_plan, int32_t *final_plan,
-                                   int32_t *boundary_plan, int32_t *boundary_lens_plan, int32_t *valid_plan,
-                                   int32_t *col_plan, const void *idx_mapping, int32_t idx_mapping_dtype,
-                                   int64_t idx_mapping_len, int32_t *persistent_cols, int32_t *persistent_accepted,
-                                   int64_t persistent_len, int64_t num_rows, int64_t plan_capacity,
-                                   int64_t null_block, int64_t spec_query_len, uint32_t flags, void *stream) {
-  if (num_groups < 1 || num_groups > GDN_PLAN_MAX_GROUPS) {
-    set_error("plan: num_groups=%d outside [1, %d]", num_groups, GDN_PLAN_MAX_GROUPS);
+namespace gdn {
+
+int make_plan_args(const gdn_plan_launch *L, PlanArgs *out) {
+  if (!L) {
+    set_error("plan: missing launch block");
     return GDN_ERR_INVALID;
   }
-  if (num_rows < 0 || num_rows > plan_capacity || plan_capacity <= 0) {
-    set_error("plan: rows=%lld outside plan capacity %lld", (long long)num_rows, (long long)plan_capacity);
+  if (L->num_groups < 1 || L->num_groups > GDN_PLAN_MAX_GROUPS || !L->groups) {
+    set_error("plan: num_groups=%d outside [1, %d]", L->num_groups, GDN_PLAN_MAX_GROUPS);
     return GDN_ERR_INVALID;
   }
-  if (spec_query_len < 1 || spec_query_len > 8) {
-    set_error("plan: spec_query_len=%lld outside [1, 8]", (long long)spec_query_len);
+  if (L->num_rows < 0 || L->num_rows > L->plan_capacity || L->plan_capacity <= 0) {
+    set_error("plan: rows=%lld outside plan capacity %lld", (long long)L->num_rows, (long long)L->plan_capacity);
     return GDN_ERR_INVALID;
   }
-  if (!sampled || !index_dtype_ok(sampled_dtype) || sampled_len < 0 || !lens_plan || !final_plan ||
-      !boundary_plan || !boundary_lens_plan) {
+  if (L->spec_query_len < 1 || L->spec_query_len > 8) {
+    set_error("plan: spec_query_len=%lld outside [1, 8]", (long long)L->spec_query_len);
+    return GDN_ERR_INVALID;
+  }
+  if (!L->sampled || !index_dtype_ok(L->sampled_dtype) || L->sampled_len < 0 || !L->lens_plan || !L->final_plan ||
+      !L->boundary_plan || !L->boundary_lens_plan) {
     set_error("plan: missing accepted counts or plan outputs");
     return GDN_ERR_INVALID;
   }
-  const bool align = flags & GDN_PLAN_ALIGN;
-  const bool grouped = flags & GDN_PLAN_GROUPED;
-  if (grouped && !source_plan) {
+  const bool align = L->flags & GDN_PLAN_ALIGN;
+  const bool grouped = L->flags & GDN_PLAN_GROUPED;
+  if (grouped && !L->source_plan) {
     set_error("plan: grouped plans store the source");
     return GDN_ERR_INVALID;
   }
-  if ((flags & GDN_PLAN_PUBLISH) && align &&
-      (!idx_mapping || !persistent_cols || !persistent_accepted || !index_dtype_ok(idx_mapping_dtype))) {
+  if ((L->flags & GDN_PLAN_PUBLISH) && align &&
+      (!L->idx_mapping || !L->persistent_cols || !L->persistent_accepted || !index_dtype_ok(L->idx_mapping_dtype))) {
     set_error("plan: publication needs idx_mapping and the persistent outputs");
     return GDN_ERR_INVALID;
   }
   PlanArgs a{};
-  a.sampled = sampled;
-  a.sampled_stride = sampled_stride;
-  a.sampled_len = sampled_len;
-  a.sampled_dtype = sampled_dtype;
-  a.num_groups = num_groups;
-  for (int i = 0; i < num_groups; ++i) {
-    const gdn_plan_group &g = groups[i];
+  a.sampled = L->sampled;
+  a.sampled_stride = L->sampled_stride;
+  a.sampled_len = L->sampled_len;
+  a.sampled_dtype = L->sampled_dtype;
+  a.num_groups = L->num_groups;
+  for (int i = 0; i < L->num_groups; ++i) {
+    const gdn_plan_group &g = L->groups[i];
     if (!g.state_indices || !g.query_start_loc || !index_dtype_ok(g.si_dtype) || !index_dtype_ok(g.qsl_dtype) ||
         (g.request_indices && !index_dtype_ok(g.map_dtype))) {
       set_error("plan: group %d lacks state indices / offsets or has a non-integer dtype", i);
@@ -300,24 +214,66 @@ extern "C" int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, i
     }
     a.groups[i] = g;
   }
-  a.source = source_plan;
-  a.lens = lens_plan;
-  a.final_ = final_plan;
-  a.boundary = boundary_plan;
-  a.boundary_lens = boundary_lens_plan;
-  a.valid = valid_plan;
-  a.col = col_plan;
-  a.idx_mapping = idx_mapping;
-  a.idx_len = idx_mapping ? idx_mapping_len : 0;
-  a.idx_dtype = idx_mapping_dtype;
-  a.flags = flags;
-  a.pcols = persistent_cols;
-  a.pacc = persistent_accepted;
-  a.plen = persistent_len;
-  a.rows = num_rows;
-  a.cap = plan_capacity;
-  a.null_block = null_block;
-  a.Q = spec_query_len;
+  a.source = L->source_plan;
+  a.lens = L->lens_plan;
+  a.final_ = L->final_plan;
+  a.boundary = L->boundary_plan;
+  a.boundary_lens = L->boundary_lens_plan;
+  a.valid = L->valid_plan;
+  a.col = L->col_plan;
+  a.idx_mapping = L->idx_mapping;
+  a.idx_len = L->idx_mapping ? L->idx_mapping_len : 0;
+  a.idx_dtype = L->idx_mapping_dtype;
+  a.flags = L->flags;
+  a.pcols = L->persistent_cols;
+  a.pacc = L->persistent_accepted;
+  a.plen = L->persistent_len;
+  a.rows = L->num_rows;
+  a.cap = L->plan_capacity;
+  a.null_block = L->null_block;
+  a.Q = L->spec_query_len;
+  *out = a;
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, int64_t sampled_stride,
+                                   int64_t sampled_len, const gdn_plan_group *groups, int32_t num_groups,
+                                   int32_t *source_plan, int32_t *lens_plan, int32_t *final_plan,
+                                   int32_t *boundary_plan, int32_t *boundary_lens_plan, int32_t *valid_plan,
+                                   int32_t *col_plan, const void *idx_mapping, int32_t idx_mapping_dtype,
+                                   int64_t idx_mapping_len, int32_t *persistent_cols, int32_t *persistent_accepted,
+                                   int64_t persistent_len, int64_t num_rows, int64_t plan_capacity,
+                                   int64_t null_block, int64_t spec_query_len, uint32_t flags, void *stream) {
+  gdn_plan_launch L{};
+  L.sampled = sampled;
+  L.sampled_stride = sampled_stride;
+  L.sampled_len = sampled_len;
+  L.sampled_dtype = sampled_dtype;
+  L.num_groups = num_groups;
+  L.groups = groups;
+  L.source_plan = source_plan;
+  L.lens_plan = lens_plan;
+  L.final_plan = final_plan;
+  L.boundary_plan = boundary_plan;
+  L.boundary_lens_plan = boundary_lens_plan;
+  L.valid_plan = valid_plan;
+  L.col_plan = col_plan;
+  L.idx_mapping = idx_mapping;
+  L.idx_mapping_len = idx_mapping_len;
+  L.idx_mapping_dtype = idx_mapping_dtype;
+  L.flags = flags;
+  L.persistent_cols = persistent_cols;
+  L.persistent_accepted = persistent_accepted;
+  L.persistent_len = persistent_len;
+  L.num_rows = num_rows;
+  L.plan_capacity = plan_capacity;
+  L.null_block = null_block;
+  L.spec_query_len = spec_query_len;
+  PlanArgs a{};
+  const int st = make_plan_args(&L, &a);
+  if (st != GDN_OK) return st;
   if (num_rows == 0) return GDN_OK;
   const unsigned blocks = unsigned((num_rows + 63) / 64);
   hipLaunchKernelGGL(plan_kernel, dim3(blocks), dim3(64), 0, static_cast<hipStream_t>(stream), a);

@@ -11,7 +11,12 @@
 // the final state after n tokens. Every chunk a thread stores was loaded by the
 // same thread before its first store, so source / final / boundary pages may
 // alias. Corrections and keys of the accepted tokens are staged in LDS.
-#include "gdn_common.cuh"
+//
+// PLANNED (gdn_recoverssm_plan_fold): the workgroup plans its own (group, row)
+// instead of reading the plan arrays, issuing the source page's loads as soon
+// as the first plan phase allows the row to commit; the first `writers`
+// workgroups of the grid store the plan arrays for the conv compaction.
+#include "plan_row.cuh"
 
 namespace gdn {
 
@@ -47,32 +52,47 @@ __device__ __forceinline__ void store_stream(void *p, const uint4 &x) {
   __builtin_nontemporal_store(v, static_cast<fold_u32x4 *>(p));
 }
 
-template <typename S, typename KT>
-__global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
+template <typename S, typename KT, bool PLANNED>
+__device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, int64_t w) {
   constexpr int E = Chunk<S>::E;
   constexpr int ITERS = 64 / E;  // chunks held per thread per batch (64 f32 values)
   extern __shared__ float lds[];
 
-  const int64_t w = blockIdx.x;
   const int64_t hv = w % a.heads;
   const int64_t row = (w / a.heads) % a.rows;
   const int64_t layer = w / (a.heads * a.rows);
-  const int64_t plan_row = (a.layer_groups ? int64_t(a.layer_groups[layer]) * a.cap : 0) + row;
-  const int64_t src = load_index(a.source, plan_row * a.source_stride, a.source_dtype);
-  const int n = a.lengths[plan_row];
-  const int64_t fin = a.finals[plan_row];
-  if (!(src > a.null_block && src < a.blocks && n > 0 && n <= a.Q && fin > a.null_block && fin < a.blocks &&
-        row < a.record_rows))
-    return;
-  const int64_t bidx = a.boundaries[plan_row];
-  const int blen = a.boundary_lens[plan_row];
-  const bool store_b = bidx > a.null_block && bidx < a.blocks && bidx != fin && blen > 0 && blen <= n;
+  const int64_t group = a.layer_groups ? int64_t(a.layer_groups[layer]) : 0;
+  const int64_t plan_row = group * a.cap + row;
+  int64_t src, fin, bidx;
+  int n, blen;
+  PlanRow pr;
+  if constexpr (PLANNED) {
+    // The values gdn_recoverssm_plan would store for this (group, row), which
+    // the fold below reads back under the same checks. A layer mapped to a
+    // group the plan does not cover folds nothing.
+    if (group < 0 || group >= p->num_groups) return;
+    const gdn_plan_group &g = p->groups[group];
+    pr = plan_begin(*p, g, row);
+    src = pr.source;
+    n = int(pr.count);
+    if (!(plan_may_commit(*p, g, pr) && src > a.null_block && src < a.blocks && n <= a.Q && row < a.record_rows))
+      return;
+    fin = bidx = a.null_block;
+    blen = 0;
+  } else {
+    src = load_index(a.source, plan_row * a.source_stride, a.source_dtype);
+    n = a.lengths[plan_row];
+    fin = a.finals[plan_row];
+    if (!(src > a.null_block && src < a.blocks && n > 0 && n <= a.Q && fin > a.null_block && fin < a.blocks &&
+          row < a.record_rows))
+      return;
+    bidx = a.boundaries[plan_row];
+    blen = a.boundary_lens[plan_row];
+  }
 
   S *base = reinterpret_cast<S *>(a.state_addrs[layer]);
   const int64_t sbs = a.state_bs[layer];
   const S *src_p = base + src * sbs + hv * a.state_head_stride;
-  S *fin_p = base + fin * sbs + hv * a.state_head_stride;
-  S *bnd_p = base + (store_b ? bidx : fin) * sbs + hv * a.state_head_stride;
 
   const int tid = threadIdx.x;
   const int KCH = a.KCH;
@@ -90,6 +110,17 @@ __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
     const int r = r0 + i * RP;
     raw[i] = (r < V && kc_ok) ? load_stream(src_p + r * vs + kc * E) : make_uint4(0, 0, 0, 0);
   }
+  if constexpr (PLANNED) {
+    const gdn_plan_group &g = p->groups[group];
+    plan_finish(*p, g, pr);
+    if (!(pr.valid && pr.final_idx > a.null_block && pr.final_idx < a.blocks)) return;
+    fin = pr.final_idx;
+    bidx = pr.boundary;
+    blen = int(pr.blen);
+  }
+  const bool store_b = bidx > a.null_block && bidx < a.blocks && bidx != fin && blen > 0 && blen <= n;
+  S *fin_p = base + fin * sbs + hv * a.state_head_stride;
+  S *bnd_p = base + (store_b ? bidx : fin) * sbs + hv * a.state_head_stride;
 
   float *corr_lds = lds;                    // [n][V]
   float *key_lds = lds + a.Q * V;           // [n][KP]
@@ -156,35 +187,49 @@ __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
   }
 }
 
-template <typename S>
-static void launch_fold_key(int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a) {
-  switch (key_dtype) {
-    case GDN_DT_BF16: hipLaunchKernelGGL((fold_kernel<S, bf16>), grid, dim3(kFoldThreads), lds, s, a); break;
-    case GDN_DT_F16: hipLaunchKernelGGL((fold_kernel<S, f16>), grid, dim3(kFoldThreads), lds, s, a); break;
-    default: hipLaunchKernelGGL((fold_kernel<S, float>), grid, dim3(kFoldThreads), lds, s, a); break;
+template <typename S, typename KT>
+__global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
+  fold_body<S, KT, false>(a, nullptr, blockIdx.x);
+}
+
+// The first `writers` workgroups store the plan (one thread per row); the rest
+// fold, each planning its own row.
+template <typename S, typename KT>
+__global__ __launch_bounds__(kFoldThreads) void plan_fold_kernel(FoldArgs a, PlanArgs p, int64_t writers) {
+  const int64_t w = blockIdx.x;
+  if (w < writers) {
+    const int64_t row = w * kFoldThreads + threadIdx.x;
+    if (row < p.rows) plan_write_row(p, row);
+    return;
   }
+  fold_body<S, KT, true>(a, &p, w - writers);
+}
+
+template <typename S>
+static void launch_fold_key(int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a,
+                            const PlanArgs *plan, int64_t writers) {
+#define GDN_FOLD_LAUNCH(KT)                                                                                   \
+  if (plan)                                                                                                   \
+    hipLaunchKernelGGL((plan_fold_kernel<S, KT>), grid, dim3(kFoldThreads), lds, s, a, *plan, writers);        \
+  else                                                                                                        \
+    hipLaunchKernelGGL((fold_kernel<S, KT>), grid, dim3(kFoldThreads), lds, s, a);
+  switch (key_dtype) {
+    case GDN_DT_BF16: GDN_FOLD_LAUNCH(bf16) break;
+    case GDN_DT_F16: GDN_FOLD_LAUNCH(f16) break;
+    default: GDN_FOLD_LAUNCH(float) break;
+  }
+#undef GDN_FOLD_LAUNCH
 }
 
 static bool float_dtype_ok(int32_t dt) { return dt == GDN_DT_F32 || dt == GDN_DT_BF16 || dt == GDN_DT_F16; }
 
-}  // namespace gdn
-
-using namespace gdn;
-
-extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, const void *key_ref,
-                                   const void *decay_ref, const int64_t *state_addrs,
-                                   const int64_t *state_block_strides, const int64_t *corr_addrs,
-                                   const int64_t *corr_block_strides, const int64_t *key_addrs,
-                                   const int64_t *key_block_strides, const int64_t *decay_addrs,
-                                   const int64_t *decay_block_strides, const int32_t *layer_groups,
-                                   const void *source, const int32_t *lengths, const int32_t *final_indices,
-                                   const int32_t *boundary_indices, const int32_t *boundary_lengths,
-                                   const int64_t *config, int64_t config_len, const gdn_fold_ext *ext,
-                                   void *stream) {
-  (void)state_ref;
-  (void)correction_ref;
-  (void)key_ref;
-  (void)decay_ref;
+// Checks the fold's configuration and fills the kernel arguments; the plan
+// arrays are filled by the caller (the fused entry has none).
+static int make_fold_args(const int64_t *state_addrs, const int64_t *state_block_strides, const int64_t *corr_addrs,
+                          const int64_t *corr_block_strides, const int64_t *key_addrs,
+                          const int64_t *key_block_strides, const int64_t *decay_addrs,
+                          const int64_t *decay_block_strides, const int32_t *layer_groups, const int64_t *config,
+                          int64_t config_len, const gdn_fold_ext *ext, FoldArgs *out, int64_t *grid, size_t *lds) {
   if (!config || config_len != GDN_FOLD_CONFIG_FIELDS || !ext) {
     set_error("fold: tiling ABI expects %d config fields and an extension block", GDN_FOLD_CONFIG_FIELDS);
     return GDN_ERR_INVALID;
@@ -194,8 +239,7 @@ extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, 
   const int64_t query_len = config[4], blocks = config[5], record_rows = config[6], cap = config[7];
   const int64_t null_block = config[8];
   if (!state_addrs || !state_block_strides || !corr_addrs || !corr_block_strides || !key_addrs ||
-      !key_block_strides || !decay_addrs || !decay_block_strides || !source || !lengths || !final_indices ||
-      !boundary_indices || !boundary_lengths) {
+      !key_block_strides || !decay_addrs || !decay_block_strides) {
     set_error("fold: missing address table or plan array");
     return GDN_ERR_INVALID;
   }
@@ -206,9 +250,8 @@ extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, 
               (long long)record_rows, (long long)cap);
     return GDN_ERR_INVALID;
   }
-  if (!float_dtype_ok(ext->state_dtype) || !float_dtype_ok(ext->key_dtype) ||
-      (ext->source_dtype != GDN_DT_I32 && ext->source_dtype != GDN_DT_I64)) {
-    set_error("fold: unsupported state/key/source dtype");
+  if (!float_dtype_ok(ext->state_dtype) || !float_dtype_ok(ext->key_dtype)) {
+    set_error("fold: unsupported state/key dtype");
     return GDN_ERR_UNSUPPORTED;
   }
   const int E = ext->state_dtype == GDN_DT_F32 ? 4 : 8;
@@ -230,13 +273,6 @@ extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, 
   a.decay_addrs = decay_addrs;
   a.decay_bs = decay_block_strides;
   a.layer_groups = layer_groups;
-  a.source = source;
-  a.source_dtype = ext->source_dtype;
-  a.source_stride = ext->source_stride;
-  a.lengths = lengths;
-  a.finals = final_indices;
-  a.boundaries = boundary_indices;
-  a.boundary_lens = boundary_lengths;
   a.rows = rows;
   a.heads = heads;
   a.ratio = heads / key_heads;
@@ -259,17 +295,24 @@ extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, 
   while (kch * E < K) kch *= 2;
   a.KCH = kch;
   a.KP = kch * E;
-  const int64_t grid = layers * rows * heads;
+  *out = a;
+  *grid = layers * rows * heads;
+  *lds = size_t(query_len) * size_t(V + a.KP) * sizeof(float);
+  return GDN_OK;
+}
+
+static int launch_fold(const gdn_fold_ext *ext, int64_t grid, size_t lds, const FoldArgs &a, const PlanArgs *plan,
+                       int64_t writers, void *stream) {
   if (grid > 0x7fffffffLL) {
     set_error("fold: grid too large");
     return GDN_ERR_UNSUPPORTED;
   }
-  const size_t lds = size_t(query_len) * size_t(V + a.KP) * sizeof(float);
   auto s = static_cast<hipStream_t>(stream);
+  const dim3 g{unsigned(grid)};
   switch (ext->state_dtype) {
-    case GDN_DT_BF16: launch_fold_key<bf16>(ext->key_dtype, dim3(unsigned(grid)), lds, s, a); break;
-    case GDN_DT_F16: launch_fold_key<f16>(ext->key_dtype, dim3(unsigned(grid)), lds, s, a); break;
-    default: launch_fold_key<float>(ext->key_dtype, dim3(unsigned(grid)), lds, s, a); break;
+    case GDN_DT_BF16: launch_fold_key<bf16>(ext->key_dtype, g, lds, s, a, plan, writers); break;
+    case GDN_DT_F16: launch_fold_key<f16>(ext->key_dtype, g, lds, s, a, plan, writers); break;
+    default: launch_fold_key<float>(ext->key_dtype, g, lds, s, a, plan, writers); break;
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
@@ -277,4 +320,81 @@ extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, 
     return GDN_ERR_LAUNCH;
   }
   return GDN_OK;
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_recoverssm_fold(void *state_ref, const void *correction_ref, const void *key_ref,
+                                   const void *decay_ref, const int64_t *state_addrs,
+                                   const int64_t *state_block_strides, const int64_t *corr_addrs,
+                                   const int64_t *corr_block_strides, const int64_t *key_addrs,
+                                   const int64_t *key_block_strides, const int64_t *decay_addrs,
+                                   const int64_t *decay_block_strides, const int32_t *layer_groups,
+                                   const void *source, const int32_t *lengths, const int32_t *final_indices,
+                                   const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                                   const int64_t *config, int64_t config_len, const gdn_fold_ext *ext,
+                                   void *stream) {
+  (void)state_ref;
+  (void)correction_ref;
+  (void)key_ref;
+  (void)decay_ref;
+  FoldArgs a{};
+  int64_t grid = 0;
+  size_t lds = 0;
+  int st = make_fold_args(state_addrs, state_block_strides, corr_addrs, corr_block_strides, key_addrs,
+                          key_block_strides, decay_addrs, decay_block_strides, layer_groups, config, config_len, ext,
+                          &a, &grid, &lds);
+  if (st != GDN_OK) return st;
+  if (!source || !lengths || !final_indices || !boundary_indices || !boundary_lengths) {
+    set_error("fold: missing address table or plan array");
+    return GDN_ERR_INVALID;
+  }
+  if (ext->source_dtype != GDN_DT_I32 && ext->source_dtype != GDN_DT_I64) {
+    set_error("fold: unsupported state/key/source dtype");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  a.source = source;
+  a.source_dtype = ext->source_dtype;
+  a.source_stride = ext->source_stride;
+  a.lengths = lengths;
+  a.finals = final_indices;
+  a.boundaries = boundary_indices;
+  a.boundary_lens = boundary_lengths;
+  return launch_fold(ext, grid, lds, a, nullptr, 0, stream);
+}
+
+extern "C" int gdn_recoverssm_plan_fold(const gdn_plan_launch *plan, void *state_ref, const void *correction_ref,
+                                        const void *key_ref, const void *decay_ref, const int64_t *state_addrs,
+                                        const int64_t *state_block_strides, const int64_t *corr_addrs,
+                                        const int64_t *corr_block_strides, const int64_t *key_addrs,
+                                        const int64_t *key_block_strides, const int64_t *decay_addrs,
+                                        const int64_t *decay_block_strides, const int32_t *layer_groups,
+                                        const int64_t *config, int64_t config_len, const gdn_fold_ext *ext,
+                                        void *stream) {
+  (void)state_ref;
+  (void)correction_ref;
+  (void)key_ref;
+  (void)decay_ref;
+  PlanArgs p{};
+  int st = make_plan_args(plan, &p);
+  if (st != GDN_OK) return st;
+  FoldArgs a{};
+  int64_t grid = 0;
+  size_t lds = 0;
+  st = make_fold_args(state_addrs, state_block_strides, corr_addrs, corr_block_strides, key_addrs, key_block_strides,
+                      decay_addrs, decay_block_strides, layer_groups, config, config_len, ext, &a, &grid, &lds);
+  if (st != GDN_OK) return st;
+  if (a.rows != p.rows || a.cap != p.cap || a.null_block != p.null_block || a.Q != p.Q) {
+    set_error("plan_fold: fold rows/capacity/null block/window (%lld/%lld/%lld/%lld) differ from the plan's "
+              "(%lld/%lld/%lld/%lld)",
+              (long long)a.rows, (long long)a.cap, (long long)a.null_block, (long long)a.Q, (long long)p.rows,
+              (long long)p.cap, (long long)p.null_block, (long long)p.Q);
+    return GDN_ERR_INVALID;
+  }
+  // layer_groups is a device table: the kernel skips a layer whose group the
+  // plan does not cover.
+  const int64_t writers = (p.rows + kFoldThreads - 1) / kFoldThreads;
+  return launch_fold(ext, grid + writers, lds, a, &p, writers, stream);
 }

@@ -111,6 +111,34 @@ class PlanGroup(ctypes.Structure):
 
 PlanGroups = PlanGroup * PLAN_MAX_GROUPS
 
+
+class PlanLaunch(ctypes.Structure):  # gdn_plan_launch: gdn_recoverssm_plan's arguments as one block
+    _fields_ = [
+        ("sampled", c_vp), ("sampled_stride", c_i64), ("sampled_len", c_i64), ("sampled_dtype", c_i32),
+        ("num_groups", c_i32), ("groups", ctypes.POINTER(PlanGroup)),
+        ("source_plan", c_vp), ("lens_plan", c_vp), ("final_plan", c_vp), ("boundary_plan", c_vp),
+        ("boundary_lens_plan", c_vp), ("valid_plan", c_vp), ("col_plan", c_vp),
+        ("idx_mapping", c_vp), ("idx_mapping_len", c_i64), ("idx_mapping_dtype", c_i32), ("flags", ctypes.c_uint32),
+        ("persistent_cols", c_vp), ("persistent_accepted", c_vp), ("persistent_len", c_i64),
+        ("num_rows", c_i64), ("plan_capacity", c_i64), ("null_block", c_i64), ("spec_query_len", c_i64),
+    ]
+
+
+def plan_launch(plan_args: tuple) -> PlanLaunch:
+    """The gdn_recoverssm_plan argument tuple (without the stream) as a PlanLaunch."""
+    (sampled, sampled_dtype, sampled_stride, sampled_len, groups, num_groups, source, lens, final, boundary,
+     boundary_lens, valid, col, idx_mapping, idx_dtype, idx_len, pcols, pacc, plen, rows, cap, null_block, window,
+     flags) = plan_args
+    return PlanLaunch(
+        sampled=sampled, sampled_stride=sampled_stride, sampled_len=sampled_len, sampled_dtype=sampled_dtype,
+        num_groups=num_groups, groups=ctypes.cast(groups, ctypes.POINTER(PlanGroup)),
+        source_plan=source, lens_plan=lens, final_plan=final, boundary_plan=boundary,
+        boundary_lens_plan=boundary_lens, valid_plan=valid, col_plan=col, idx_mapping=idx_mapping,
+        idx_mapping_len=idx_len, idx_mapping_dtype=idx_dtype, flags=flags, persistent_cols=pcols,
+        persistent_accepted=pacc, persistent_len=plen, num_rows=rows, plan_capacity=cap, null_block=null_block,
+        spec_query_len=window,
+    )
+
 _LIB = None
 _LOCK = threading.Lock()
 
@@ -150,6 +178,10 @@ def load() -> ctypes.CDLL:
         ]
         lib.gdn_recoverssm_fold.restype = ctypes.c_int
         lib.gdn_recoverssm_fold.argtypes = [c_vp] * 18 + [P_i64, c_i64, ctypes.POINTER(FoldExt), c_vp]
+        lib.gdn_recoverssm_plan_fold.restype = ctypes.c_int
+        lib.gdn_recoverssm_plan_fold.argtypes = [ctypes.POINTER(PlanLaunch)] + [c_vp] * 13 + [
+            P_i64, c_i64, ctypes.POINTER(FoldExt), c_vp,
+        ]
         lib.gdn_recoverssm_plan.restype = ctypes.c_int
         lib.gdn_recoverssm_plan.argtypes = [
             c_vp, c_i32, c_i64, c_i64,  # sampled
@@ -185,6 +217,7 @@ def exported_symbols() -> tuple[str, ...]:
         "gdn_recoverssm_verify_gated",
         "gdn_recoverssm_verify_deferred",
         "gdn_recoverssm_fold",
+        "gdn_recoverssm_plan_fold",
         "gdn_recoverssm_plan",
         "gdn_recoverssm_conv_compact",
         "gdn_recoverssm_publish",

@@ -23,6 +23,7 @@ import torch
 from . import _native as N
 from .kernels import (
     NULL_BLOCK_ID,
+    _fuse_plan_fold,
     _LaunchSpec,
     _make_fold_spec,
     _ptr_table,
@@ -182,7 +183,13 @@ class GroupedCommitBucket:
     def _strides(self, tensors, dim):
         return torch.tensor([t.stride(dim) for t in tensors], dtype=torch.int64, device=self.device)
 
-    def make_specs(self, entries, sampled, idx_mapping, persistent_cols, persistent_accepted, *, publish_align=True):
+    def make_specs(
+        self, entries, sampled, idx_mapping, persistent_cols, persistent_accepted, *, publish_align=True,
+        fuse_plan_fold=True,
+    ):
+        """Launch specs of one bucket's commit: the fused plan + fold, then the
+        conv compaction (with ``fuse_plan_fold=False``: plan, conv, fold as
+        three launches, the reference's order, identical results)."""
         contexts = tuple(e.context for e in entries)
         if len(contexts) != len(self.contexts) or any(a is not b for a, b in zip(contexts, self.contexts)):
             raise ValueError("grouped recovery bucket belongs to a different KV epoch")
@@ -337,7 +344,10 @@ class GroupedCommitBucket:
             plan=(self.length, self.final, self.boundary, self.boundary_len),
             refs=(rr, kr, dr),
         )
-        return plan, compact, fold
+        if not fuse_plan_fold:
+            return plan, compact, fold
+        # One launch plans and folds; the conv compaction reads the stored plan after it.
+        return _fuse_plan_fold(plan, fold), compact
 
 
 class GroupedCommitCoordinator:

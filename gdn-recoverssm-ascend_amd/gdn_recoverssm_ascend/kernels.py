@@ -1053,6 +1053,10 @@ class GDNRecoverSSMCommitContext:
             refs=(rr, kr, dr),
         )
         specs.append(fold_spec)
+        if _fold_source is None:
+            # One launch plans and folds; the conv compaction, which reads the
+            # stored plan, follows it.
+            specs = [_fuse_plan_fold(plan_spec, fold_spec)] + specs[1:-1]
         if _collect is not None:
             _collect.extend(specs)
         else:
@@ -1103,6 +1107,21 @@ class GDNRecoverSSMCommitContext:
             _collect.append(spec)
         else:
             spec.launch()
+
+
+def _fuse_plan_fold(plan: _LaunchSpec, fold: _LaunchSpec) -> _LaunchSpec:
+    """``gdn_recoverssm_plan_fold``: the plan launch and the fold launch that
+    reads its arrays, as one launch with identical results (every fold
+    workgroup plans its own row; extra workgroups store the plan arrays)."""
+    launch = N.plan_launch(plan.args)
+    # fold arguments: 4 reference tensors, 8 tables, layer_groups, source,
+    # 4 plan arrays, config, config length, extension
+    args = (ctypes.byref(launch),) + tuple(fold.args[:13]) + tuple(fold.args[18:])
+    spec = _LaunchSpec(
+        "plan_fold", _lib().gdn_recoverssm_plan_fold, args, fold.device, keepalive=(plan.keepalive, fold.keepalive, launch)
+    )
+    spec.config = fold.config
+    return spec
 
 
 def _make_fold_spec(

@@ -217,6 +217,45 @@ int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, int64_t samp
                         int64_t num_rows, int64_t plan_capacity, int64_t null_block, int64_t spec_query_len,
                         uint32_t flags, void *stream);
 
+/* The arguments of gdn_recoverssm_plan as one block, for the fused plan + fold
+ * entry below (same meaning, same checks). */
+typedef struct gdn_plan_launch {
+  const void *sampled;
+  int64_t sampled_stride;
+  int64_t sampled_len;
+  int32_t sampled_dtype;
+  int32_t num_groups;
+  const gdn_plan_group *groups; /* HOST pointer to num_groups entries */
+  int32_t *source_plan, *lens_plan, *final_plan, *boundary_plan, *boundary_lens_plan, *valid_plan, *col_plan;
+  const void *idx_mapping;
+  int64_t idx_mapping_len;
+  int32_t idx_mapping_dtype;
+  uint32_t flags;
+  int32_t *persistent_cols, *persistent_accepted;
+  int64_t persistent_len;
+  int64_t num_rows, plan_capacity, null_block, spec_query_len;
+} gdn_plan_launch;
+
+/* Plan and fold in one launch (no counterpart entry in the reference, which
+ * launches its plan and fold kernels one after the other: kernels.py:1036-1072
+ * then :1222-1324, grouped_commit.py:377-480). Every fold workgroup plans its
+ * own (group, row) from the step's metadata and starts streaming the source
+ * page before the block-table lookups return; extra workgroups store the plan
+ * arrays (and the align publication) exactly as gdn_recoverssm_plan does, for
+ * the conv compaction that follows. Results are identical to
+ * gdn_recoverssm_plan followed by gdn_recoverssm_fold reading the plan it
+ * stored (`source` = the group's state indices, or the plan's source for a
+ * grouped plan). The fold arguments are those of gdn_recoverssm_fold without
+ * the plan arrays; config[0] (rows) must equal plan->num_rows and config[7]
+ * (capacity) plan->plan_capacity. */
+int gdn_recoverssm_plan_fold(const gdn_plan_launch *plan, void *state_ref, const void *correction_ref,
+                             const void *key_ref, const void *decay_ref, const int64_t *state_addrs,
+                             const int64_t *state_block_strides, const int64_t *corr_addrs,
+                             const int64_t *corr_block_strides, const int64_t *key_addrs,
+                             const int64_t *key_block_strides, const int64_t *decay_addrs,
+                             const int64_t *decay_block_strides, const int32_t *layer_groups,
+                             const int64_t *config, int64_t config_len, const gdn_fold_ext *ext, void *stream);
+
 /* Conv-state compaction (grouped_commit.py:225-322 / kernels.py:1075-1169).
  * Per-layer DEVICE tables: base addresses, block / dim / token strides
  * (elements). element_bytes is 2 or 4. `source` as in gdn_recoverssm_fold.

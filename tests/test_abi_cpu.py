@@ -68,6 +68,24 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert st == N.GDN_ERR_INVALID
     st = lib.gdn_recoverssm_publish(None, 1, None, 3, 1, 1, None, 3, 1, None, None, 1, 1, None)
     assert st == N.GDN_ERR_INVALID
+    # fused plan + fold: the plan block is checked first, then the fold
+    # configuration, then that both describe the same rows
+    launch = N.PlanLaunch(num_groups=0, groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)))
+    st = lib.gdn_recoverssm_plan_fold(ctypes.byref(launch), *([None] * 13), N.i64_array([0] * 17), 17,
+                                      ctypes.byref(fext), None)
+    assert st == N.GDN_ERR_INVALID and b"num_groups" in lib.gdn_recoverssm_last_error()
+    g0 = groups[0]
+    g0.state_indices = g0.query_start_loc = 8  # never dereferenced: the call is rejected before a launch
+    g0.si_dtype = g0.qsl_dtype = 3
+    launch = N.PlanLaunch(sampled=8, sampled_len=4, sampled_dtype=3, num_groups=1,
+                          groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), lens_plan=8, final_plan=8,
+                          boundary_plan=8, boundary_lens_plan=8, num_rows=4, plan_capacity=4, spec_query_len=4)
+    tables = [8] * 8
+    fcfg = N.i64_array([4, 1, 4, 2, 4, 16, 4, 8, 0, 128 * 128, 128, 512, 128, 256, 128, 4, 1])
+    fext1 = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1)
+    st = lib.gdn_recoverssm_plan_fold(ctypes.byref(launch), None, None, None, None, *tables, None, fcfg, 17,
+                                      ctypes.byref(fext1), None)
+    assert st == N.GDN_ERR_INVALID and b"differ from the plan" in lib.gdn_recoverssm_last_error()
 
 
 def test_zero_rows_is_a_noop_without_touching_the_device():
@@ -89,6 +107,9 @@ int main(void) {
   printf("gdn_plan_group %zu\n", sizeof(gdn_plan_group));
   printf("gdn_gating_ext %zu\n", sizeof(gdn_gating_ext));
   printf("gdn_pending_commit %zu\n", sizeof(gdn_pending_commit));
+  printf("gdn_plan_launch %zu\n", sizeof(gdn_plan_launch));
+  F(gdn_plan_launch, groups) F(gdn_plan_launch, col_plan) F(gdn_plan_launch, idx_mapping_dtype)
+  F(gdn_plan_launch, flags) F(gdn_plan_launch, persistent_len) F(gdn_plan_launch, spec_query_len)
   F(gdn_pending_commit, record_rows) F(gdn_pending_commit, decay_strides) F(gdn_pending_commit, key_per_value_head)
   F(gdn_gating_ext, softplus_beta) F(gdn_gating_ext, softplus_threshold)
   F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
@@ -113,12 +134,14 @@ def test_ctypes_struct_layout_matches_c_compiler():
     assert int(got["gdn_plan_group"]) == ctypes.sizeof(N.PlanGroup)
     assert int(got["gdn_gating_ext"]) == ctypes.sizeof(N.GatingExt)
     assert int(got["gdn_pending_commit"]) == ctypes.sizeof(N.PendingCommit)
+    assert int(got["gdn_plan_launch"]) == ctypes.sizeof(N.PlanLaunch)
     for key, value in got.items():
         if "." not in key:
             continue
         struct, fld = key.split(".")
         cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup,
-               "gdn_gating_ext": N.GatingExt, "gdn_pending_commit": N.PendingCommit}[struct]
+               "gdn_gating_ext": N.GatingExt, "gdn_pending_commit": N.PendingCommit,
+               "gdn_plan_launch": N.PlanLaunch}[struct]
         assert getattr(cls, fld).offset == int(value), key
 
 

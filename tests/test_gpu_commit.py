@@ -244,7 +244,7 @@ def test_grouped_bucket_two_groups_reordered_rows(dev, align):
     accp = torch.full((7,), 7, dtype=torch.int32)
     cols_d, accp_d = cols.to(dev), accp.to(dev)
     specs = bucket.make_specs(entries, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
-    assert [s.name for s in specs] == ["plan", "conv", "fold"]
+    assert [s.name for s in specs] == ["plan_fold", "conv"]
     for s in specs:
         s.launch()
     torch.cuda.synchronize()
@@ -310,7 +310,8 @@ def test_coordinator_seven_groups_three_buckets_and_publication(dev):
     coord = GroupedCommitCoordinator()
     coord.commit(metas, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
     torch.cuda.synchronize()
-    assert coord.last_group_count == 7 and coord.last_launch_count == 10
+    # three buckets of (plan + fold, conv) and one publication across buckets
+    assert coord.last_group_count == 7 and coord.last_launch_count == 7
     assert [len(b.contexts) for b in coord._buckets.values()] == [3, 3, 1]
     want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, True, B)
     assert cols_d.cpu().tolist() == want["persistent_cols"].tolist()
@@ -323,3 +324,70 @@ def test_coordinator_seven_groups_three_buckets_and_publication(dev):
                                boundary_len=want["boundary_len"][seg], rows=B, num_blocks=G["NB"], record_rows=B)
         targeted = set(want["final"][seg].tolist()) | set(want["boundary"][seg].tolist())
         _check_states(devs[gi][0], wstate, torch.float32, targeted)
+
+
+@pytest.mark.parametrize("align", [False, True])
+def test_fused_plan_fold_equals_plan_then_fold(dev, align):
+    """The fused entry (every fold workgroup plans its own row) against the
+    plan kernel followed by the fold reading the stored plan: plan arrays,
+    pages and conv states bit-identical, including padded and short rows."""
+    B = 12
+    G = _group(B, 2, 4, 128, 128, 4, 2, align=align, seed=91 + align, qlens=[4] * 9 + [2, 0, 4])
+    G["src"][7] = -1  # a padded row
+    runs = []
+    for fused in (True, False):
+        ckpts, convs, recs = _to_dev(G, dev)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=16)
+        src = G["src"].to(dev)
+        kw = dict(block_table=None if not align else G["table"].to(dev),
+                  num_computed_tokens=None if not align else G["C"].to(dev), mamba_block_size=G["Bk"])
+        if not fused:
+            kw["_fold_source"] = src  # the reference's three launches: plan, conv, fold
+        ctx.commit(G["acc"].to(dev), src, G["qsl"].to(dev), **kw)
+        torch.cuda.synchronize()
+        names = [sp.name for sp in ctx._last_specs]
+        assert names == (["plan_fold", "conv"] if fused else ["plan", "conv", "fold"])
+        runs.append(([c.cpu() for c in ckpts], [c.cpu() for c in convs],
+                     [t[:B].cpu() for t in (ctx.plan_source, ctx.commit_lens, ctx.final_state_indices,
+                                            ctx.boundary_state_indices, ctx.boundary_recovery_lens, ctx.align_valid,
+                                            ctx.align_col)]))
+    (pa, ca, qa), (pb, cb, qb) = runs
+    for x, y in zip(qa, qb):
+        assert torch.equal(x, y)
+    for x, y in zip(pa + ca, pb + cb):
+        assert torch.equal(x, y)
+    assert int(qa[1].gt(0).sum()) > 0
+    if align:
+        assert int(qa[4].gt(0).sum()) > 0, "the case must exercise boundary snapshots"
+
+
+@pytest.mark.parametrize("align", [False, True])
+def test_grouped_fused_equals_three_launches(dev, align):
+    B = 6
+    request_rows = [2, 0, 5, 1, 4, 3]
+    sampled = torch.tensor([4, 0, 3, 1, 2, 4], dtype=torch.int32)
+    results = []
+    for fuse in (True, False):
+        groups = [_index_by_request(_group(B, 2, 4, 128, 128, 4, 2, align=align, seed=160 + g, page_offset=10 * g),
+                                    request_rows) for g in range(2)]
+        contexts, entries, devs = [], [], []
+        for G in groups:
+            ckpts, convs, recs = _to_dev(G, dev)
+            ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+            contexts.append(ctx)
+            devs.append((ckpts, convs))
+            entries.append(_entry(G, ctx, dev, request_rows))
+        bucket = GroupedCommitBucket(tuple(contexts))
+        cols_d = torch.full((7,), -9, dtype=torch.int32, device=dev)
+        accp_d = torch.full((7,), 7, dtype=torch.int32, device=dev)
+        mapping = torch.tensor([3, 1, -1, 0, 5, 2], dtype=torch.int32, device=dev)
+        specs = bucket.make_specs(entries, sampled.to(dev), mapping, cols_d, accp_d, fuse_plan_fold=fuse)
+        assert len(specs) == (2 if fuse else 3)
+        for sp in specs:
+            sp.launch()
+        torch.cuda.synchronize()
+        results.append([t.cpu() for t in (bucket.source, bucket.length, bucket.final, bucket.boundary,
+                                          bucket.boundary_len, bucket.valid, bucket.col, cols_d, accp_d)]
+                       + [t.cpu() for d in devs for part in d for t in part])
+    for x, y in zip(*results):
+        assert torch.equal(x, y)
