@@ -42,14 +42,25 @@ constexpr int kFoldThreads = 256;
 // directions are non-temporal: they bypass the caches' normal retention and
 // leave them to the records. Measured on MI355X this shortens a verify + plan
 // + fold step by ~13% against plain loads and stores.
+//
+// Each (page, head) tile is addressed through a buffer resource covering
+// exactly its V rows: a thread keeps one 32-bit offset and the pass step goes
+// in the scalar offset, so no per-chunk 64-bit addresses occupy registers
+// (four times the occupancy of flat addressing), and rows past V or chunks
+// past K read zero and drop their stores without a branch.
 typedef unsigned fold_u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 load_stream(const void *p) {
-  const fold_u32x4 v = __builtin_nontemporal_load(static_cast<const fold_u32x4 *>(p));
+constexpr int kFoldNT = 2;                  // buffer cache policy: non-temporal
+constexpr int kFoldOutOfRange = 0x7ffff000;  // past any tile's extent (<= 1 MiB)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fold_tile(const void *p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 load_stream(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  const fold_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kFoldNT);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ void store_stream(void *p, const uint4 &x) {
+__device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int voff, int soff, const uint4 &x) {
   const fold_u32x4 v = {x.x, x.y, x.z, x.w};
-  __builtin_nontemporal_store(v, static_cast<fold_u32x4 *>(p));
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, kFoldNT);
 }
 
 template <typename S, typename KT, bool PLANNED>
@@ -92,7 +103,10 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
 
   S *base = reinterpret_cast<S *>(a.state_addrs[layer]);
   const int64_t sbs = a.state_bs[layer];
-  const S *src_p = base + src * sbs + hv * a.state_head_stride;
+  const int V = a.V;
+  const int64_t vs = a.state_v_stride;
+  const int tile_bytes = int(V * vs * int64_t(sizeof(S)));
+  const __amdgpu_buffer_rsrc_t rsrc = fold_tile(base + src * sbs + hv * a.state_head_stride, tile_bytes);
 
   const int tid = threadIdx.x;
   const int KCH = a.KCH;
@@ -100,16 +114,15 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   const int r0 = tid / KCH;
   const int RP = kFoldThreads / KCH;  // rows covered by one pass of the workgroup
   const bool kc_ok = kc * E < a.K;
-  const int V = a.V;
-  const int64_t vs = a.state_v_stride;
+  // Byte offset of the thread's chunk in pass 0 (rows past V fall outside the
+  // tile's extent); pass i adds i * step in the scalar offset.
+  const int voff = kc_ok ? int((r0 * vs + kc * E) * int64_t(sizeof(S))) : kFoldOutOfRange;
+  const int step = int(RP * vs * int64_t(sizeof(S)));
 
   // Issue the first batch of state loads before staging the records.
   uint4 raw[ITERS];
 #pragma unroll
-  for (int i = 0; i < ITERS; ++i) {
-    const int r = r0 + i * RP;
-    raw[i] = (r < V && kc_ok) ? load_stream(src_p + r * vs + kc * E) : make_uint4(0, 0, 0, 0);
-  }
+  for (int i = 0; i < ITERS; ++i) raw[i] = load_stream(rsrc, voff, i * step);
   if constexpr (PLANNED) {
     const gdn_plan_group &g = p->groups[group];
     plan_finish(*p, g, pr);
@@ -119,8 +132,9 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
     blen = int(pr.blen);
   }
   const bool store_b = bidx > a.null_block && bidx < a.blocks && bidx != fin && blen > 0 && blen <= n;
-  S *fin_p = base + fin * sbs + hv * a.state_head_stride;
-  S *bnd_p = base + (store_b ? bidx : fin) * sbs + hv * a.state_head_stride;
+  const __amdgpu_buffer_rsrc_t rfin = fold_tile(base + fin * sbs + hv * a.state_head_stride, tile_bytes);
+  const __amdgpu_buffer_rsrc_t rbnd =
+      fold_tile(base + (store_b ? bidx : fin) * sbs + hv * a.state_head_stride, tile_bytes);
 
   float *corr_lds = lds;                    // [n][V]
   float *key_lds = lds + a.Q * V;           // [n][KP]
@@ -148,10 +162,7 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   for (int first = 0; first < passes; first += ITERS) {
     if (first > 0) {
 #pragma unroll
-      for (int i = 0; i < ITERS; ++i) {
-        const int r = r0 + (first + i) * RP;
-        raw[i] = (r < V && kc_ok) ? load_stream(src_p + r * vs + kc * E) : make_uint4(0, 0, 0, 0);
-      }
+      for (int i = 0; i < ITERS; ++i) raw[i] = load_stream(rsrc, voff, (first + i) * step);
     }
     float h[ITERS][E];
 #pragma unroll
@@ -172,18 +183,12 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
         }
         if (store_b && t + 1 == blen) {
 #pragma unroll
-          for (int i = 0; i < ITERS; ++i) {
-            const int r = r0 + (first + i) * RP;
-            if (r < V && kc_ok) store_stream(bnd_p + r * vs + kc * E, pack16<S>(h[i]));
-          }
+          for (int i = 0; i < ITERS; ++i) store_stream(rbnd, voff, (first + i) * step, pack16<S>(h[i]));
         }
       }
     }
 #pragma unroll
-    for (int i = 0; i < ITERS; ++i) {
-      const int r = r0 + (first + i) * RP;
-      if (r < V && kc_ok) store_stream(fin_p + r * vs + kc * E, pack16<S>(h[i]));
-    }
+    for (int i = 0; i < ITERS; ++i) store_stream(rfin, voff, (first + i) * step, pack16<S>(h[i]));
   }
 }
 
@@ -261,6 +266,15 @@ static int make_fold_args(const int64_t *state_addrs, const int64_t *state_block
     set_error("fold: K=%lld V=%lld unsupported (K <= 256 and a multiple of %d, V <= 1024, K contiguous, "
               "16-byte aligned rows)",
               (long long)K, (long long)V, E);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  // A (page, head) tile is addressed as V rows of config[10] elements through
+  // one buffer resource: rows must not overlap and the tile must stay far
+  // below the out-of-range offset.
+  const int64_t tile_bytes = V * config[10] * (E == 4 ? 4 : 2);
+  if (config[10] < K || tile_bytes > (int64_t(1) << 27)) {
+    set_error("fold: state row stride %lld unsupported (at least K=%lld, tile of V rows <= 128 MiB)",
+              (long long)config[10], (long long)K);
     return GDN_ERR_UNSUPPORTED;
   }
   FoldArgs a{};
