@@ -196,7 +196,8 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   int j = 1;
   while (4 * E * j < K) j *= 2;
   const int qm = Q <= 1 ? 1 : Q <= 2 ? 2 : Q <= 4 ? 4 : 8;
-  a.NVT = int32_t((V + kTileRows - 1) / kTileRows);
+  const int tile = verify_tile_rows(pending != nullptr);
+  a.NVT = int32_t((V + tile - 1) / tile);
   if (int64_t(a.NVT) * value_heads > 0x7fffffffLL) {
     set_error("verify: grid too large");
     return GDN_ERR_UNSUPPORTED;

@@ -19,7 +19,8 @@
 // matrix cores, and each 64-row half runs its recurrence while the next
 // half's loads are outstanding. Everything the recurrence needs from memory
 // (v, gates) is loaded before the first state block, because the vector memory
-// counter retires in issue order.
+// counter retires in issue order. The deferred-commit variant (DEFER) works
+// on 64-row tiles: four blocks, one recurrence.
 //
 // MFMA operand layout (16x16x4, wave64): A lane l = (row l%16, k-slot l/16),
 // B lane l = (k-slot l/16, column l%16), D lane l register r = (row
@@ -72,6 +73,12 @@ struct VerifyArgs {
 
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
 constexpr int kTileRows = 128;     // eight MFMA row blocks of 16 rows
+// The deferred-commit kernels stream half tiles: a wave that also stores the
+// folded state lives twice as long per row, and with twice as many, shorter
+// waves the launch's tail is shorter (measured: 232 against 236 us per step;
+// the plain verify is 3 us faster with whole tiles).
+constexpr int kDeferTileRows = 64;
+__host__ __device__ constexpr int verify_tile_rows(bool deferred) { return deferred ? kDeferTileRows : kTileRows; }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -194,7 +201,8 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   constexpr int KP = 4 * E * J;        // K padded to 4 k-slots x J chunks x E
   constexpr int NV = 2 * QM;           // used MFMA columns (<= 16)
   constexpr int MP = KP + 4;           // LDS row pitch of the k/q vectors (bank spread)
-  constexpr int NRB = kTileRows / 16;  // 16-row MFMA blocks per tile
+  constexpr int TILE = verify_tile_rows(DEFER);
+  constexpr int NRB = TILE / 16;  // 16-row MFMA blocks per tile (8 or 4)
   __shared__ float m_lds[NV][MP];
   __shared__ float gram_lds[QM][NV];
   __shared__ float d_lds[64][NV + 1];  // GEMV results of one 64-row half tile
@@ -210,7 +218,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const int h = hv / ratio;
   const int lane = threadIdx.x;
   const int V = a.V, K = a.K;
-  const int row0 = vt * kTileRows;
+  const int row0 = vt * TILE;
   const int Q = a.Q;
 
   const int64_t bos = ld_idx(a.qsl, int64_t(b) * a.qsl_s, a.qsl_i64);
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     for (int t = 0; t < Q; ++t) {
       const int64_t tok = bos + t;
       if (!(t < qlen && tok >= 0 && tok < a.tokens)) continue;
-      for (int r = lane; r < kTileRows; r += kVerifyThreads)
+      for (int r = lane; r < TILE; r += kVerifyThreads)
         if (row0 + r < V) st_f32_or<A>(a.out, tok * a.out_ts + out_base + r, a.out_f32 != 0, 0.0f);
     }
     if (!pend) return;
@@ -351,7 +359,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   // per chunk and the block step in soffset. Rows >= V lie past the resource's
   // extent and read as zero; chunks >= K get an out-of-range offset.
   // Rows of block rb: rb*16 + li; the lane loads chunks 4j + ls of its row.
-  const int tile_rows = V - row0 < kTileRows ? V - row0 : kTileRows;
+  const int tile_rows = V - row0 < TILE ? V - row0 : TILE;
   const int tile_bytes = tile_rows * a.state_vs * int(sizeof(S));
   auto tile_rsrc = [&](int64_t page, bool use) {
     const S *tp = static_cast<const S *>(a.state) + page * a.state_bs + int64_t(hv) * a.state_hs +
@@ -617,7 +625,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     fold_block(rb + 1, bufB, pcB);
     gemv_block(rb + 1, bufB);
     if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
-    if (rb + 2 == NRB / 2) load_v(1);
+    if (NRB == 8 && rb + 2 == NRB / 2) load_v(1);  // a half tile has no second half
     if ((rb + 2) % 4 == 0 && row0 + (rb - 2) * 16 < V) recurrence((rb + 2) / 4 - 1);
   }
 }
