@@ -371,7 +371,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
-              "(the verify/commit path shards by rows and heads with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the verify/commit path shards by rows and heads with no exchange step)", file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.join(HERE, "gdn-recoverssm-ascend_amd"))
     from gdn_recoverssm_ascend import workloads as W
