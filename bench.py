@@ -370,7 +370,7 @@ def decode_loop(args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the verify/commit path shards by rows and heads with no exchange step)", file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.join(HERE, "gdn-recoverssm-ascend_amd"))

@@ -40,7 +40,7 @@ extern "C" {
 /* Status codes. */
 #define GDN_OK 0
 #define GDN_ERR_INVALID 1     /* geometry / dtype / stride violation; nothing launched */
-#define GDN_ERR_UNSUPPORTED 2 /* outside what this build implements; nothing launched */
+#define GDN_ERR_UNSUPPORTED 2 /* outside what this library implements; nothing launched */
 #define GDN_ERR_LAUNCH 3      /* the HIP runtime rejected the launch */
 
 /* Element type codes for tensors whose dtype is not fixed by the ABI. */
@@ -57,7 +57,7 @@ extern "C" {
 /* Fold tiling: the 17 fields of GDN_FOLD_FIELDS, csrc/common.h:37-54. */
 #define GDN_FOLD_CONFIG_FIELDS 17
 
-/* What this build adds over the reference's K=V=128 native specialisation
+/* What this library adds over the reference's K=V=128 native specialisation
  * (csrc/ops.cpp:100-141): dimensions, dtypes and layout flags that the
  * reference's Triton kernel took as constexprs (kernels.py:534-545). */
 typedef struct gdn_verify_ext {
