@@ -229,6 +229,8 @@ class GroupedCommitBucket:
             host_rows = tuple(getattr(x, "request_rows", ()))
             if len(host_rows) == rows and any(r < 0 or r >= sampled.numel() or r >= idx_mapping.numel() for r in host_rows):
                 raise ValueError("native request mapping exceeds the sampled batch")
+        if self.device.type != "cuda":
+            raise ValueError("grouped recovery runs on a HIP device")
         lib = N.load()
         groups = N.PlanGroups()
         for gi, (x, c) in enumerate(zip(p, contexts)):

@@ -935,6 +935,7 @@ class GDNRecoverSSMCommitContext:
             ),
             "commit inputs must be on the same device",
         )
+        _require(_dev.type == "cuda", "the commit runs on a HIP device")
         align = block_table is not None
         lib = _lib()
         grp = N.PlanGroups()
