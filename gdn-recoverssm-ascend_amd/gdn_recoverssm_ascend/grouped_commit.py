@@ -1,14 +1,18 @@
-"""Step-owned grouped recovery: one plan, one conv pass and one SSM fold per bucket.
+"""Step-owned grouped recovery: one plan + SSM fold launch and one conv pass per bucket.
 
 Host side of the post-sampling commit, keeping the reference plugin's API
 (``gdn_recoverssm_ascend/grouped_commit.py``): ``CommitEntry``,
-``GroupedCommitBucket``, ``GroupedCommitCoordinator`` and ``prepare_grouped_commit``. The three kernels are the gfx950 HIP entry points
-``gdn_recoverssm_plan``, ``gdn_recoverssm_conv_compact`` and
-``gdn_recoverssm_fold``; a multi-bucket align step adds ``gdn_recoverssm_publish``.
+``GroupedCommitBucket``, ``GroupedCommitCoordinator`` and
+``prepare_grouped_commit``. A bucket launches the gfx950 HIP entry points
+``gdn_recoverssm_plan_fold`` (the reference's plan and fold kernels as one
+launch) and ``gdn_recoverssm_conv_compact``; ``make_specs(...,
+fuse_plan_fold=False)`` gives the reference's three launches
+(``gdn_recoverssm_plan``, conv, ``gdn_recoverssm_fold``) instead. A
+multi-bucket align step adds ``gdn_recoverssm_publish``.
 
 A bucket holds up to three homogeneous cache groups (the reference's bucket
-width, grouped_commit.py:947-954) so that launch counts and bucket boundaries
-match the reference coordinator exactly.
+width, grouped_commit.py:947-954), so bucket boundaries match the reference
+coordinator exactly.
 """
 
 from __future__ import annotations

@@ -9,8 +9,11 @@ argument meaning and error behaviour follow the reference plugin's
   checkpoint (reference kernels.py:700-928);
 * ``ReplayRecordBuffers`` / ``record_nbytes`` / ``record_geometry_bytes`` -- the
   typed-SoA record layout and its byte accounting (kernels.py:166-294);
-* ``GDNRecoverSSMCommitContext`` -- per-layer address tables and the
-  plan -> conv compaction -> fold commit (kernels.py:1399-2052).
+* ``GDNRecoverSSMCommitContext`` -- per-layer address tables and the commit
+  (kernels.py:1399-2052): the plan and the fold in one launch
+  (``gdn_recoverssm_plan_fold``), then the conv compaction that reads the
+  stored plan; ``commit_deferred`` plans now and leaves the fold to the next
+  verify (``gdn_recoverssm_verify_deferred``).
 
 Every launch goes to the hand-written HIP kernels of ``libgdn_recoverssm_hip.so``
 through its C ABI (``_native``). Validation happens before any launch and raises
@@ -43,7 +46,8 @@ _COUNTS: Counter = Counter()
 
 
 def counts() -> dict:
-    """Launch counters per entry point (``verify``, ``plan``, ``conv``, ``fold``, ``publish``)."""
+    """Launch counters per entry point (``verify``, ``plan``, ``conv``, ``fold``, ``plan_fold``, ``publish``);
+    ``prepared_<name>`` counts compile-only preparations."""
     return dict(_COUNTS)
 
 
@@ -185,7 +189,7 @@ class _LaunchSpec:
     ``launch()`` submits it; ``compile_only()`` checks that the AOT library is
     loaded and the entry point exists without touching device memory (the
     kernels are compiled ahead of time). ``name`` is the entry point
-    (``verify`` / ``plan`` / ``conv`` / ``fold`` / ``publish``).
+    (``verify`` / ``plan`` / ``conv`` / ``fold`` / ``plan_fold`` / ``publish``).
     """
 
     name: str
