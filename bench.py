@@ -153,6 +153,60 @@ def measured_traffic(workload, kernel):
     return k["hbm_bytes"], os.path.relpath(path, HERE)
 
 
+def other_configs(args, timer, skip):
+    """The verify + commit step of the other single-layer configurations
+    (B=64 from a 512-page pool; B=256 at Q=1; B=256 at Q=8 with geometric
+    acceptance), each timed like the main region on its own synthetic batch."""
+    import torch
+
+    from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+
+    dev = torch.device("cuda:0")
+    res = {}
+    for name in ("pool512_b64", "decode_q1_b256", "skewed_q8_b256"):
+        if name == skip:
+            continue
+        w = W.make_workload(name, gen_device="cuda").to(dev)
+        s = w.spec
+        B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+        inp, m = w.inputs[0], w.meta
+        align = m.block_table is not None
+        rec = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, [rec], spec_query_len=Q,
+                                                      max_num_reqs=B)
+        out = torch.empty(1, w.tokens, HV, V, dtype=inp.v.dtype, device=dev)
+        specs: list = []
+        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0],
+                              replay_cache=rec, query_start_loc=m.query_start_loc, state_indices=m.state_indices,
+                              spec_query_len=Q, out=out, _collect=specs)
+        specs += list(ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
+                                            block_table=m.block_table if align else None,
+                                            num_computed_tokens=m.num_computed if align else None,
+                                            mamba_block_size=m.block_size if align else None, commit_conv=False))
+        for _ in range(args.warmup):
+            for sp in specs:
+                sp.launch()
+        e0, e1 = timer.event(), timer.event()
+        torch.cuda.synchronize()
+        timer.record(e0)
+        for _ in range(args.steps):
+            for sp in specs:
+                sp.launch()
+        timer.record(e1)
+        torch.cuda.synchronize()
+        ms = timer.elapsed(e0, e1) / args.steps
+        nb = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices,
+                        ctx.boundary_recovery_lens)
+        total = nb["verify"] + nb["commit"]
+        res[name] = {"rows": B, "window": Q, "us_per_step": round(ms * 1e3, 2), "bytes": total,
+                     "gbs": round(total / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del w, rec, ctx, out, specs
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(w_cpu, threads):
     """FP32 torch oracle on the host cores: one full verify + plan + fold step."""
     import torch
@@ -562,6 +616,7 @@ def main():
                     "ordinary step's algorithmic bytes by this step time",
         }
     gbs = total / (step_ms * 1e-3) / 1e9
+    others = None if args.kernel_only else other_configs(args, timer, s.name)
 
     per_kernel = {}
     for name, ms in kernel_ms.items():
@@ -635,6 +690,7 @@ def main():
         "cpu_baseline": cpu,
         "fused_gating": fused,
         "deferred_commit": deferred,
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
     return 0
