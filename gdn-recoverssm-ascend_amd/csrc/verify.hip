@@ -68,8 +68,11 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   };
   if (!window_ok(config[8], heads * K, act_b) || !window_ok(config[9], heads * K, act_b) ||
       !window_ok(config[10], value_heads * V, act_b) || !window_ok(config[11], value_heads, 4) ||
-      !window_ok(config[12], value_heads, 4)) {
-    set_error("verify: activation token strides must be non-negative and span under 2 GiB per window");
+      !window_ok(config[12], value_heads, 4) ||
+      !window_ok(config[25], value_heads * V, ext->out_dtype == GDN_DT_F32 ? 4 : act_b) ||
+      !window_ok(config[18], V, 4)) {
+    set_error("verify: activation / output / correction token strides must be non-negative and span under 2 GiB "
+              "per window");
     return GDN_ERR_UNSUPPORTED;
   }
   if (gating && (!float_dt_ok(gating->a_log_dtype) || !float_dt_ok(gating->dt_bias_dtype) ||

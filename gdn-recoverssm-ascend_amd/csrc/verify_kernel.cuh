@@ -588,32 +588,45 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       for (int r = 0; r < 4; ++r) d_lds[rr + r][li] = acc[r];
     }
   };
+  // Outputs and corrections go out through buffer stores that are issued for
+  // every token and lane (an invalid one gets an out-of-range offset and is
+  // dropped): a store skipped on some path would make the wait counts of the
+  // loads still in flight assume it, and drain the pipeline at the next block.
   const bool out_f32 = a.out_f32 != 0;
+  const __amdgpu_buffer_rsrc_t rout = make_rsrc(a.out, (bos * a.out_ts + out_base) * (out_f32 ? 4 : AS));
+  const __amdgpu_buffer_rsrc_t rcorr =
+      make_rsrc(a.corr, (int64_t(b) * a.corr_rs + int64_t(hv) * a.corr_hs + row0) * 4);
   auto recurrence = [&](int half) {
     wave_lds_sync();  // d_lds (and, on the first half, gram_lds) complete
     const int lrow = half * 64 + lane;
-    const bool row_ok = row0 + lrow < V;
+    int row_ok = row0 + lrow < V;
+    asm volatile("" : "+v"(row_ok));  // per-lane offsets below, not branches
     float u[QM], wq[QM];
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
       u[t] = d_lds[lane][t];
       wq[t] = d_lds[lane][QM + t];
     }
-    float *corr_row = a.corr + int64_t(b) * a.corr_rs + int64_t(hv) * a.corr_hs + row0 + lrow;
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
-      if ((valid_mask >> t) & 1u) {
-        const float d = dec[t];
-        const float c = (vv[half][t] - d * u[t]) * bet[t];
+      const bool tv = (valid_mask >> t) & 1u;
+      const float d = dec[t];
+      const float c = tv ? (vv[half][t] - d * u[t]) * bet[t] : 0.0f;
+      if (tv) {
 #pragma unroll
         for (int j = t + 1; j < QM; ++j) u[j] = __builtin_fmaf(c, gram_lds[t][j], d * u[j]);
 #pragma unroll
         for (int j = t; j < QM; ++j) wq[j] = __builtin_fmaf(c, gram_lds[t][QM + j], d * wq[j]);
-        if (row_ok) {
-          st_f32_or<A>(a.out, (bos + t) * a.out_ts + out_base + lrow, out_f32, wq[t]);
-          if (rec_ok) corr_row[int64_t(t) * a.corr_ts] = c;
-        }
       }
+      const bool st = tv && row_ok;
+      const int oel = t * int(a.out_ts) + lrow;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(wq[t]), rout, st && out_f32 ? oel * 4 : kOutOfRange,
+                                            0, 0);
+      if constexpr (sizeof(A) == 2)
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f32<A>(wq[t])), rout,
+                                              st && !out_f32 ? oel * AS : kOutOfRange, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(c), rcorr,
+                                            st && rec_ok ? (t * a.corr_ts + lrow) * 4 : kOutOfRange, 0, 0);
     }
     wave_lds_sync();  // d_lds may be overwritten by the next half
   };
@@ -626,7 +639,9 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     gemv_block(rb + 1, bufB);
     if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
     if (NRB == 8 && rb + 2 == NRB / 2) load_v(1);  // a half tile has no second half
-    if ((rb + 2) % 4 == 0 && row0 + (rb - 2) * 16 < V) recurrence((rb + 2) / 4 - 1);
+    // Every half runs its recurrence, also one past V (its rows store nothing):
+    // skipping it would be a path without its stores.
+    if ((rb + 2) % 4 == 0) recurrence((rb + 2) / 4 - 1);
   }
 }
 
