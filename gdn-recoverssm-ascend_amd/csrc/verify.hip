@@ -45,7 +45,7 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   const int64_t K = ext->key_dim, V = ext->value_dim;
   const int64_t state_bs = config[13], state_hs = config[14], state_vs = config[15];
   if (K < 1 || K > 256 || K % E != 0 || V < 1 || state_vs % E != 0 || state_hs % E != 0 || state_bs % E != 0 ||
-      !fits_i32(state_hs) || !fits_i32(state_vs * V) ||
+      !fits_i32(state_hs) || !fits_i32(state_vs * V) || state_vs * (ext->state_dtype == GDN_DT_F32 ? 4 : 2) >= (1 << 24) ||
       (reinterpret_cast<uintptr_t>(state) & 15u) != 0) {
     set_error("verify: state layout K=%lld V=%lld unsupported (K <= 256, multiple of %d, 16-byte aligned rows)",
               (long long)K, (long long)V, E);

@@ -373,7 +373,10 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const __amdgpu_buffer_rsrc_t rfin = tile_rsrc(pfin, pend);
   const __amdgpu_buffer_rsrc_t rbnd = tile_rsrc(pbnd, pstore_b);
   const int row_bytes = a.state_vs * int(sizeof(S));
-  const int lane_off = li * row_bytes + ls * 16;
+  // A 24-bit product (row_bytes < 2^24, checked on the host): a full multiply
+  // here became a 64-bit multiply-add whose unused high addend was a register
+  // with a load in flight, and waiting for it held back the first state loads.
+  const int lane_off = int(__umul24(unsigned(li), unsigned(row_bytes))) + ls * 16;
   // The pending corrections of the lane's row, fetched with each block.
   const __amdgpu_buffer_rsrc_t rpc =
       make_rsrc(a.p_corr, (int64_t(prow) * a.p_corr_rs + int64_t(hv) * a.p_corr_hs + row0) * 4);
