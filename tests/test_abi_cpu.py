@@ -150,3 +150,16 @@ def test_config_field_counts_match_reference_abi():
     text = open(HEADER).read()
     assert "#define GDN_VERIFY_CONFIG_FIELDS 28" in text and N.VERIFY_CONFIG_FIELDS == 28
     assert "#define GDN_FOLD_CONFIG_FIELDS 17" in text and N.FOLD_CONFIG_FIELDS == 17
+
+
+def test_native_caller_is_built_against_this_header():
+    """The native C-ABI caller the GPU tests run (tests/capi/capi_step) starts
+    and rejects a missing argument before any HIP call."""
+    import os
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "capi", "capi_step")
+    if not os.path.exists(exe):
+        pytest.skip("tests/capi/capi_step is built by __graft_entry__.build()")
+    r = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=60)
+    assert r.returncode == 2 and b"usage" in r.stdout
