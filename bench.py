@@ -3,7 +3,8 @@
 
 One step = ``gdn_recoverssm_verify`` over the whole speculative batch, then the
 commit of the accepted prefix (``GDNRecoverSSMCommitContext.commit``: plan +
-fold, conv compaction timed separately) on the align-mode workload
+fold in one launch; the same step followed by the conv compaction is reported
+beside it) on the align-mode workload
 ``align_b256``: 256 sequences, 16 key / 32 value heads, K = V = 128, Q = 4, FP32
 state pages, bf16 activations, block size 64 with ~25% of the rows crossing a
 block boundary, accepted lengths uniform in {0..4}, 6 padded rows.
@@ -48,7 +49,7 @@ def parse():
                     help="decode-loop workloads: fold each commit into the next step's verify")
     ap.add_argument("--loop-steps", type=int, default=None,
                     help="decode-loop workloads: speculative steps to time (default: the workload's own)")
-    ap.add_argument("--kernel-only", action="store_true", help="skip the separate conv-compaction timing")
+    ap.add_argument("--kernel-only", action="store_true", help="time the step and its kernels only (no conv, gated, deferred or other-configuration lines)")
     ap.add_argument("--copy-calibration", type=int, default=0,
                     help="also run a device copy of this many MiB (PMC scale calibration)")
     return ap.parse_args()
@@ -454,10 +455,12 @@ def main():
     gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0], replay_cache=rec,
                           query_start_loc=m.query_start_loc, state_indices=m.state_indices, spec_query_len=Q, out=out,
                           _collect=verify_specs)
-    commit_specs = ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
-                                         block_table=m.block_table if align else None,
-                                         num_computed_tokens=m.num_computed if align else None,
-                                         mamba_block_size=m.block_size if align else None, commit_conv=True)
+    align_kw = dict(block_table=m.block_table if align else None,
+                    num_computed_tokens=m.num_computed if align else None,
+                    mamba_block_size=m.block_size if align else None)
+    # The step's commit: plan + fold in one launch (the conv compaction is
+    # outside the step's byte model and is measured after it further down).
+    commit_specs = ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc, commit_conv=False, **align_kw)
     by_name = {sp.name: sp for sp in commit_specs}
     step_specs = verify_specs + [by_name["plan_fold"]]
 
@@ -498,22 +501,26 @@ def main():
     marked_step_ms = timer.elapsed(marks[0][0], marks[-1][-1]) / args.steps
     kernel_ms = {n: sum(timer.elapsed(ev[j], ev[j + 1]) for ev in marks) / args.steps for j, n in enumerate(names)}
 
-    # Conv-state compaction runs in the same commit but is outside the byte
-    # model; timed on its own after the region.
+    # The whole commit as the reference runs it also compacts the conv states:
+    # the same K steps with the conv compaction launched after plan + fold
+    # (it reads the plan that launch stores).
+    full_ms = None
     if not args.kernel_only:
-        reps = max(10, args.steps // 2)
-        conv = by_name["conv"]
-        ev = [(timer.event(), timer.event()) for _ in range(reps)]
-        # A ~10 us kernel finishes before the host submits the next one: hold
-        # the stream with a spin kernel so the launches queue up and run back
-        # to back, and each pair of events brackets the kernel alone.
-        torch.cuda._sleep(10_000_000)
-        for a, b in ev:
-            timer.record(a)
-            conv.launch()
-            timer.record(b)
+        full_specs = verify_specs + list(
+            ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc, commit_conv=True, **align_kw))
+        assert [sp.name for sp in full_specs[len(verify_specs):]] == ["plan_fold", "conv"]
+        for _ in range(args.warmup):
+            for sp in full_specs:
+                sp.launch()
+        f0, f1 = timer.event(), timer.event()
         torch.cuda.synchronize()
-        kernel_ms["conv"] = sum(timer.elapsed(a, b) for a, b in ev) / reps
+        timer.record(f0)
+        for _ in range(args.steps):
+            for sp in full_specs:
+                sp.launch()
+        timer.record(f1)
+        torch.cuda.synchronize()
+        full_ms = timer.elapsed(f0, f1) / args.steps
 
     # The gated verify (gating and q/k L2 norm fused in) against the plain one,
     # each over back-to-back launches on the same batch.
@@ -617,6 +624,21 @@ def main():
         }
     gbs = total / (step_ms * 1e-3) / 1e9
     others = None if args.kernel_only else other_configs(args, timer, s.name)
+    full_step = None
+    if full_ms is not None:
+        conv_dim, conv_len = w.conv_states[0].shape[1:]
+        conv_b = conv_bytes(s, ctx.commit_lens[:B].cpu(), ctx.boundary_state_indices[:B].cpu(),
+                            ctx.boundary_recovery_lens[:B].cpu(), w.num_pages, conv_dim, conv_len - Q + 1,
+                            w.conv_states[0].element_size())
+        full_step = {
+            "us_per_step": round(full_ms * 1e3, 2),
+            "conv_bytes": conv_b,
+            "gbs": round((total + conv_b) / (full_ms * 1e-3) / 1e9, 1),
+            "frac": round((total + conv_b) / (full_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "conv_us": round((full_ms - step_ms) * 1e3, 2),
+            "note": "verify, plan + fold, then the conv compaction (the reference's whole commit); conv_bytes "
+                    "counts the kept history positions read and written, conv_us is the step-time difference",
+        }
 
     per_kernel = {}
     for name, ms in kernel_ms.items():
@@ -689,6 +711,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fused_gating": fused,
+        "with_conv_compaction": full_step,
         "deferred_commit": deferred,
         "other_configs": others,
     }

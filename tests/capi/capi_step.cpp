@@ -4,11 +4,12 @@
 // which writes the problem to <dir> and checks what this program writes back
 // against the CPU oracle.
 //
-// <dir>/meta.txt holds "name value" lines (B T H HV K V Q NB W BS SCALE); the
-// inputs are raw little-endian arrays: q, k, v (bf16 bits), g, beta (f32),
-// state (f32 [NB, HV, V, K]), qsl, idx, accepted, table ([B, W]), computed
-// (i32). Outputs: out (bf16 bits), corr, decay (f32), key (bf16 bits), the
-// committed state (f32) and the plan arrays (i32).
+// <dir>/meta.txt holds "name value" lines (B T H HV K V Q NB W BS CD CW SCALE);
+// the inputs are raw little-endian arrays: q, k, v (bf16 bits), g, beta (f32),
+// state (f32 [NB, HV, V, K]), conv (bf16 bits [NB, CD, CW]), qsl, idx,
+// accepted, table ([B, W]), computed (i32). Outputs: out (bf16 bits), corr,
+// decay (f32), key (bf16 bits), the committed state (f32), the compacted conv
+// states (bf16 bits) and the plan arrays (i32).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -98,7 +99,7 @@ int main(int argc, char **argv) {
   }
   const int64_t B = int64_t(m["B"]), T = int64_t(m["T"]), H = int64_t(m["H"]), HV = int64_t(m["HV"]);
   const int64_t K = int64_t(m["K"]), V = int64_t(m["V"]), Q = int64_t(m["Q"]), NB = int64_t(m["NB"]);
-  const int64_t W = int64_t(m["W"]), BS = int64_t(m["BS"]);
+  const int64_t W = int64_t(m["W"]), BS = int64_t(m["BS"]), CD = int64_t(m["CD"]), CW = int64_t(m["CW"]);
   const float scale = float(m["SCALE"]);
   if (gdn_recoverssm_abi_version() != 1) {
     std::fprintf(stderr, "ABI version %d\n", gdn_recoverssm_abi_version());
@@ -111,6 +112,7 @@ int main(int argc, char **argv) {
   void *g = upload(dir, "g", size_t(T * HV * 4));
   void *beta = upload(dir, "beta", size_t(T * HV * 4));
   void *state = upload(dir, "state", size_t(NB * HV * V * K * 4));
+  void *conv = upload(dir, "conv", size_t(NB * CD * CW * 2));
   void *qsl = upload(dir, "qsl", size_t((B + 1) * 4));
   void *idx = upload(dir, "idx", size_t(B * 4));
   void *accepted = upload(dir, "accepted", size_t(B * 4));
@@ -151,7 +153,8 @@ int main(int argc, char **argv) {
                                GDN_VERIFY_CONFIG_FIELDS, scale, &vext, stream),
          "gdn_recoverssm_verify");
 
-  // Commit: plan + fold in one launch (align mode, one group, no request mapping).
+  // Commit: plan + fold in one launch (align mode, one group, no request
+  // mapping), then the conv compaction reading the plan it stored.
   int32_t *plan[7];
   for (auto &p : plan) p = static_cast<int32_t *>(zeros(size_t(B * 4)));
   gdn_plan_group grp{};
@@ -192,10 +195,13 @@ int main(int argc, char **argv) {
   pl.null_block = 0;
   pl.spec_query_len = Q;
   pl.flags = GDN_PLAN_ALIGN;
-  // Per-layer tables (one layer): base addresses and block strides, on the device.
-  const int64_t host_tables[8] = {reinterpret_cast<int64_t>(state), HV * V * K, reinterpret_cast<int64_t>(corr),
-                                  HV * Q * V, reinterpret_cast<int64_t>(key), H * Q * K,
-                                  reinterpret_cast<int64_t>(decay), HV * Q};
+  // Per-layer tables (one layer), on the device: base addresses and block
+  // strides of state, corrections, keys and decays, then the conv states'
+  // base address and block / dim / token strides.
+  const int64_t host_tables[12] = {reinterpret_cast<int64_t>(state), HV * V * K, reinterpret_cast<int64_t>(corr),
+                                   HV * Q * V, reinterpret_cast<int64_t>(key), H * Q * K,
+                                   reinterpret_cast<int64_t>(decay), HV * Q, reinterpret_cast<int64_t>(conv),
+                                   CD * CW, CW, 1};
   int64_t *tables = nullptr;
   HIP_OK(hipMalloc(&tables, sizeof(host_tables)));
   HIP_OK(hipMemcpy(tables, host_tables, sizeof(host_tables), hipMemcpyHostToDevice));
@@ -213,6 +219,10 @@ int main(int argc, char **argv) {
                                   tables + 4, tables + 5, tables + 6, tables + 7, nullptr, fcfg,
                                   GDN_FOLD_CONFIG_FIELDS, &fext, stream),
          "gdn_recoverssm_plan_fold");
+  abi_ok(gdn_recoverssm_conv_compact(tables + 8, tables + 9, tables + 10, tables + 11, idx, GDN_DT_I32, 1, plan[1],
+                                     plan[2], plan[3], plan[4], nullptr, B, 0, B, 1, CD, CW - Q + 1, CW, NB, 2, 1,
+                                     stream),
+         "gdn_recoverssm_conv_compact");
   HIP_OK(hipStreamSynchronize(stream));
 
   download(dir, "out_out", out, size_t(T * HV * V * 2));
@@ -220,6 +230,7 @@ int main(int argc, char **argv) {
   download(dir, "out_key", key, size_t(B * H * Q * K * 2));
   download(dir, "out_decay", decay, size_t(B * HV * Q * 4));
   download(dir, "out_state", state, size_t(NB * HV * V * K * 4));
+  download(dir, "out_conv", conv, size_t(NB * CD * CW * 2));
   const char *plan_names[7] = {"out_source", "out_lens", "out_final", "out_boundary", "out_blen", "out_valid",
                                "out_col"};
   for (int i = 0; i < 7; ++i) download(dir, plan_names[i], plan[i], size_t(B * 4));

@@ -1,15 +1,18 @@
 """The C ABI on its own: a native program (tests/capi/capi_step.cpp, built by
 the build step) allocates device buffers with hipMalloc, calls
-gdn_recoverssm_verify and gdn_recoverssm_plan_fold the way a non-Python
+gdn_recoverssm_verify, gdn_recoverssm_plan_fold and
+gdn_recoverssm_conv_compact the way a non-Python
 serving runtime would, and writes the results back. Nothing of the Python
 package runs on the device in this test; the program is started as a child
 process and its outputs are checked against the CPU oracle.
 
 Problem: an align-mode step (prefix-cache block table, boundary crossings,
-padded rows) at K=V=128, Q=4, 16 rows, 2 key heads, 4 value heads.
-Bar: plan arrays bit-exact; bf16 outputs within 1e-2 norm-wise; corrections
-within 1e-5 norm-wise; keys bit-exact; decays within 3e-7 relative; committed
-FP32 pages within max-abs 1e-5 relative; every other page bit-identical.
+padded rows) at K=V=128, Q=4, 16 rows, 2 key heads, 4 value heads, with the
+conv states of the same pages compacted from the plan the commit stored.
+Bar: plan arrays and conv states bit-exact; bf16 outputs within 1e-2
+norm-wise; corrections within 1e-5 norm-wise; keys bit-exact; decays within
+3e-7 relative; committed FP32 pages within max-abs 1e-5 relative; every other
+page bit-identical.
 """
 
 import os
@@ -56,11 +59,13 @@ def test_native_caller_step_against_oracle(tmp_path, seed):
     print(f"native C-ABI step: seed={seed} B={B} T={T} pages={NB} table width={Wd}", flush=True)
 
     d = str(tmp_path)
-    meta = dict(B=B, T=T, H=H, HV=HV, K=K, V=V, Q=Q, NB=NB, W=Wd, BS=m.block_size, SCALE=scale)
+    conv = w.conv_states[0]
+    CD, CW = int(conv.shape[1]), int(conv.shape[2])
+    meta = dict(B=B, T=T, H=H, HV=HV, K=K, V=V, Q=Q, NB=NB, W=Wd, BS=m.block_size, CD=CD, CW=CW, SCALE=scale)
     with open(os.path.join(d, "meta.txt"), "w") as f:
         f.writelines(f"{k} {v!r}\n" for k, v in meta.items())
     i32 = lambda t: t.to(torch.int32)  # noqa: E731
-    arrays = dict(q=inp.q, k=inp.k, v=inp.v, g=inp.g.float(), beta=inp.beta.float(), state=w.checkpoints[0],
+    arrays = dict(q=inp.q, k=inp.k, v=inp.v, g=inp.g.float(), beta=inp.beta.float(), state=w.checkpoints[0], conv=conv,
                   qsl=i32(m.query_start_loc), idx=i32(m.state_indices), accepted=i32(m.accepted),
                   table=i32(m.block_table), computed=i32(m.num_computed))
     for name, t in arrays.items():
@@ -112,3 +117,8 @@ def test_native_caller_step_against_oracle(tmp_path, seed):
     untouched[targeted] = False
     assert torch.equal(got[untouched], ck0[untouched]), "pages outside the commit changed"
     assert_state_close(got[targeted], want[targeted], "committed pages")
+
+    want_conv = O.oracle_conv_compact([conv], source=m.state_indices, lengths=n, final=plan["final"],
+                                      boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                                      history=CW - Q + 1, num_blocks=NB, rows=B, align=True)[0]
+    assert torch.equal(rd("conv", np.int16, (NB, CD, CW)), want_conv), "conv states differ"

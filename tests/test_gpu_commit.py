@@ -391,3 +391,43 @@ def test_grouped_fused_equals_three_launches(dev, align):
                        + [t.cpu() for d in devs for part in d for t in part])
     for x, y in zip(*results):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("case", ["f32", "odd_dim", "token_major", "many_tiles"])
+def test_conv_layouts_fused_and_three_launches(dev, case):
+    """Conv compaction after the fused plan + fold and after the three
+    separate launches, against the oracle: FP32 conv states (24-byte windows,
+    moved element by element), an odd channel count, token-major pages
+    (element by element) and pages spanning several workgroups with a partial
+    last one."""
+    B, Q = 10, 4
+    G = _group(B, 2, 4, 128, 128, Q, 2, align=True, seed=300 + len(case))
+    dim = {"odd_dim": 41, "many_tiles": 3000}.get(case, CONV_DIM)
+    dtype = torch.float32 if case == "f32" else torch.bfloat16
+    gen = torch.Generator().manual_seed(17)
+    convs = [torch.randn(G["NB"], dim, HIST + Q - 1, generator=gen).to(dtype) for _ in range(2)]
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=Q, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    want = O.oracle_conv_compact(convs, source=G["src"], lengths=plan["commit_lens"], final=plan["final"],
+                                 boundary=plan["boundary"], boundary_len=plan["boundary_len"], history=HIST,
+                                 num_blocks=G["NB"], rows=B, align=True)
+    assert int(plan["boundary_len"].gt(0).sum()) > 0 and int(plan["commit_lens"].gt(0).sum()) > 0
+    token_major = case == "token_major"
+    for fused in (True, False):
+        ckpts, _, recs = _to_dev(G, dev)
+        # token-major pages are [blocks, window, dim] in memory
+        dconvs = [(c.transpose(1, 2).contiguous() if token_major else c).to(dev) for c in convs]
+        ctx = GDNRecoverSSMCommitContext.from_tensors(dconvs, ckpts, recs, spec_query_len=Q, max_num_reqs=B,
+                                                      conv_dim_first=not token_major)
+        src = G["src"].to(dev)
+        kw = dict(block_table=G["table"].to(dev), num_computed_tokens=G["C"].to(dev), mamba_block_size=G["Bk"])
+        if not fused:
+            kw["_fold_source"] = src  # plan, conv, fold as three launches
+        ctx.commit(G["acc"].to(dev), src, G["qsl"].to(dev), **kw)
+        torch.cuda.synchronize()
+        assert [sp.name for sp in ctx._last_specs] == (["plan_fold", "conv"] if fused else ["plan", "conv", "fold"])
+        for li, (got, w) in enumerate(zip(dconvs, want)):
+            got = got.cpu()
+            if token_major:
+                got = got.transpose(1, 2)
+            assert torch.equal(got, w), f"{case} fused={fused} layer {li}: conv states differ"
