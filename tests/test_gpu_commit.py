@@ -13,6 +13,7 @@ import torch
 import gdn_oracle as O
 from gdn_recoverssm_ascend.grouped_commit import CommitEntry, GroupedCommitBucket, GroupedCommitCoordinator
 from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers
+import sweep_cases as SC
 from gpu_helpers import assert_state_close
 
 pytestmark = pytest.mark.gpu
@@ -431,3 +432,40 @@ def test_conv_layouts_fused_and_three_launches(dev, case):
             if token_major:
                 got = got.transpose(1, 2)
             assert torch.equal(got, w), f"{case} fused={fused} layer {li}: conv states differ"
+
+
+@pytest.mark.parametrize("case", range(SC.COMMIT_CASES))
+def test_random_configurations(dev, case):
+    """Seeded draws of every commit option together: head dims, GQA ratio,
+    window, layers, none / align mode and block size, state and key dtypes,
+    packed records, short and empty windows, a padded row."""
+    c = SC.commit_case(case)
+    print(f"commit sweep case {case}: {c}", flush=True)
+    B, Q, align = c["B"], c["Q"], c["align"]
+    G = _group(B, c["H"], c["HV"], c["K"], c["V"], Q, c["L"], align=align, seed=c["seed"], Bk=c["Bk"],
+               key_dtype=c["key_dtype"], state_dtype=c["state_dtype"], packed=c["packed"], qlens=c["qlens"])
+    if c["padded"]:
+        G["src"][B // 2] = -1
+    ckpts, convs, recs = _to_dev(G, dev)
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=Q, max_num_reqs=B + 3)
+    ctx.commit(G["acc"].to(dev), G["src"].to(dev), G["qsl"].to(dev),
+               block_table=G["table"].to(dev) if align else None,
+               num_computed_tokens=G["C"].to(dev) if align else None, mamba_block_size=G["Bk"])
+    torch.cuda.synchronize()
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=Q, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    for key, t in (("commit_lens", ctx.commit_lens), ("final", ctx.final_state_indices),
+                   ("boundary", ctx.boundary_state_indices), ("boundary_len", ctx.boundary_recovery_lens),
+                   ("align_valid", ctx.align_valid), ("align_col", ctx.align_col)):
+        assert t[:B].cpu().tolist() == plan[key].tolist(), f"plan {key} differs"
+    corrs, keys, decays = _planes(G)
+    want = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=G["src"], lengths=plan["commit_lens"],
+                         final=plan["final"], boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                         rows=B, num_blocks=G["NB"], record_rows=B)
+    targeted = set(plan["final"].tolist()) | set(plan["boundary"].tolist())
+    _check_states(ckpts, want, c["state_dtype"], targeted)
+    want_conv = O.oracle_conv_compact(G["convs"], source=G["src"], lengths=plan["commit_lens"], final=plan["final"],
+                                      boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                                      history=HIST, num_blocks=G["NB"], rows=B, align=align)
+    for li, (got, w) in enumerate(zip(convs, want_conv)):
+        assert torch.equal(got.cpu(), w), f"layer {li}: conv states differ"

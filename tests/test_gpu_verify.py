@@ -11,6 +11,7 @@ import torch
 import gdn_oracle as O
 from gdn_recoverssm_ascend import workloads as W
 from gdn_recoverssm_ascend.kernels import ReplayRecordBuffers, gdn_recoverssm_verify
+import sweep_cases as SC
 from gpu_helpers import CORR_TOL, OUT_TOL, assert_norm_close
 
 pytestmark = pytest.mark.gpu
@@ -307,3 +308,18 @@ def test_gated_verify_fuses_gating_and_l2norm(dev, ab_dtype, param_dtype):
     key = rec.key.cpu()
     m_k = rw[:, None, :, None].expand_as(key)
     torch.testing.assert_close(key[m_k].double(), res.key[m_k].double(), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("case", range(SC.VERIFY_CASES))
+def test_random_configurations(dev, case):
+    """Seeded draws of every verify option together: head dims, GQA ratio,
+    window, ragged / null / out-of-range rows, activation, state, key, beta
+    and output dtypes, packed records, in-kernel L2 norm, index dtypes and
+    column views, record rows below the batch, explicit scale."""
+    c = SC.verify_case(case)
+    p = c["problem"]
+    print(f"verify sweep case {case}: {p} {c['run']}", flush=True)
+    P = _problem(p["B"], p["H"], p["HV"], p["K"], p["V"], p["Q"], qlens=p["qlens"], seed=p["seed"], act=p["act"],
+                 state_dtype=p["state_dtype"], null_rows=p["null_rows"], oob_rows=p["oob_rows"],
+                 normalise=p["normalise"])
+    _run_and_check(P, dev, **c["run"])

@@ -15,6 +15,8 @@ from types import SimpleNamespace
 import pytest
 import torch
 
+import sweep_cases as SC
+
 from gdn_recoverssm_ascend import kernels as Kmod
 from gdn_recoverssm_ascend.grouped_commit import CommitEntry, GroupedCommitBucket, GroupedCommitCoordinator
 from gdn_recoverssm_ascend.kernels import (
@@ -179,3 +181,34 @@ def test_coordinator_rejects_mixed_and_disagreeing_groups():
     with pytest.raises(ValueError, match="must agree"):
         GroupedCommitCoordinator().commit([e.metadata for e in disagree], *inputs)
     assert dict(Kmod.counts()) == before
+
+
+@pytest.mark.parametrize("case", range(SC.VERIFY_CASES))
+def test_verify_sweep_cases_pass_host_validation(case):
+    """Every seeded verify configuration of the GPU sweep is accepted by the
+    host checks (on the CPU the call stops only at the device check)."""
+    import test_gpu_verify as TV
+
+    c = SC.verify_case(case)
+    p = c["problem"]
+    P = TV._problem(p["B"], p["H"], p["HV"], p["K"], p["V"], p["Q"], qlens=p["qlens"], seed=p["seed"], act=p["act"],
+                    state_dtype=p["state_dtype"], null_rows=p["null_rows"], oob_rows=p["oob_rows"],
+                    normalise=p["normalise"])
+    with pytest.raises(ValueError, match="HIP device"):
+        TV._run_and_check(P, torch.device("cpu"), **c["run"])
+
+
+@pytest.mark.parametrize("case", range(SC.COMMIT_CASES))
+def test_commit_sweep_cases_pass_host_validation(case):
+    """The same for the seeded commit configurations."""
+    import test_gpu_commit as TC
+
+    c = SC.commit_case(case)
+    B, Q, align = c["B"], c["Q"], c["align"]
+    G = TC._group(B, c["H"], c["HV"], c["K"], c["V"], Q, c["L"], align=align, seed=c["seed"], Bk=c["Bk"],
+                  key_dtype=c["key_dtype"], state_dtype=c["state_dtype"], packed=c["packed"], qlens=c["qlens"])
+    ckpts, convs, recs = TC._to_dev(G, torch.device("cpu"))
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=Q, max_num_reqs=B + 3)
+    with pytest.raises(ValueError, match="HIP device"):
+        ctx.commit(G["acc"], G["src"], G["qsl"], block_table=G["table"] if align else None,
+                   num_computed_tokens=G["C"] if align else None, mamba_block_size=G["Bk"])
