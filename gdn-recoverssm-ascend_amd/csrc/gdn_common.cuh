@@ -32,8 +32,15 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float x) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return bf16{uint16_t(u >> 16)};
 }
+// The conversion starts from the rounded FP32 value: left to itself the
+// compiler folds a multiply-add that produced x into the conversion (one
+// mixed-precision FMA rounded once, straight to f16), which differs in the last
+// bit now and then from computing in FP32 and then storing in f16.
 template <>
-__device__ __forceinline__ f16 from_f32<f16>(float x) { return f16(x); }
+__device__ __forceinline__ f16 from_f32<f16>(float x) {
+  asm volatile("" : "+v"(x));
+  return f16(x);
+}
 
 // Load one element of a runtime-typed tensor as f32 (activations, gates).
 __device__ __forceinline__ float load_as_f32(const void *p, int64_t i, int dt) {
@@ -111,8 +118,8 @@ __device__ __forceinline__ uint4 pack16<f16>(const float *in) {
   uint32_t w[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    w[i] = uint32_t(__builtin_bit_cast(uint16_t, f16(in[2 * i]))) |
-           (uint32_t(__builtin_bit_cast(uint16_t, f16(in[2 * i + 1]))) << 16);
+    w[i] = uint32_t(__builtin_bit_cast(uint16_t, from_f32<f16>(in[2 * i]))) |
+           (uint32_t(__builtin_bit_cast(uint16_t, from_f32<f16>(in[2 * i + 1]))) << 16);
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 

@@ -110,3 +110,36 @@ def test_deferred_commit_equals_ordinary_flow(dev, seed, empty_row):
     # the comparison is not vacuous: commits happened and crossed boundaries
     assert sum(int((h["plan"][0] > 0).sum()) for h in ref) > 0
     assert sum(int((h["plan"][2] > 0).sum()) for h in ref) > 0
+
+
+@pytest.mark.parametrize("K,V,Q,H,HV,act", [
+    (64, 100, 3, 1, 4, torch.bfloat16),
+    (256, 64, 8, 2, 2, torch.bfloat16),
+    (32, 192, 1, 2, 8, torch.float16),
+    (136, 48, 5, 3, 6, torch.float32),
+    (96, 16, 6, 1, 1, torch.bfloat16),
+])
+def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act):
+    """The same equality over head dims off the 128 x 128 tile (partial
+    64-row half tiles, K padded to whole chunks), windows 1-8, GQA ratios 1-4
+    and every activation dtype."""
+    steps = 3
+    w = W.make_workload("decode_loop_l48", layers=2, rows=6, key_heads=H, value_heads=HV, key_dim=K, value_dim=V,
+                        window=Q, act_dtype=act, steps=steps, max_position=256, block_size=8, padded_rows=1,
+                        seed=K + V + Q)
+    s = w.spec
+    print(f"deferred shapes: K={K} V={V} Q={Q} H={H} HV={HV} act={act}", flush=True)
+    gen = torch.Generator().manual_seed(K * V + Q)
+    acc_steps = [W.sample_accepted(s, s.rows, gen) for _ in range(steps)]
+    qsl_steps = [w.meta.query_start_loc.clone() for _ in range(steps)]
+    ref, ref_pages, ref_convs = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
+    got, got_pages, got_convs = _flow(w, dev, acc_steps, qsl_steps, deferred=True)
+    for step, (a, b) in enumerate(zip(ref, got)):
+        for name in ("out", "corr", "key", "decay", "plan"):
+            for li, (x, y) in enumerate(zip(a[name], b[name])):
+                assert torch.equal(x, y), f"step {step} {name} [{li}] differs"
+    for li, (x, y) in enumerate(zip(ref_pages, got_pages)):
+        assert torch.equal(x, y), f"layer {li}: pages differ after the flush"
+    for li, (x, y) in enumerate(zip(ref_convs, got_convs)):
+        assert torch.equal(x, y), f"layer {li}: conv states differ"
+    assert sum(int((h["plan"][0] > 0).sum()) for h in ref) > 0
