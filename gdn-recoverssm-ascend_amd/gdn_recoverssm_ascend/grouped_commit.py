@@ -17,7 +17,6 @@ coordinator exactly.
 
 from __future__ import annotations
 
-import ctypes
 import logging
 from dataclasses import dataclass
 from typing import Any
