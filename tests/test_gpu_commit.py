@@ -469,3 +469,66 @@ def test_random_configurations(dev, case):
                                       history=HIST, num_blocks=G["NB"], rows=B, align=align)
     for li, (got, w) in enumerate(zip(convs, want_conv)):
         assert torch.equal(got.cpu(), w), f"layer {li}: conv states differ"
+
+
+@pytest.mark.parametrize("n_groups,align,B,seed", [(1, True, 5, 1), (2, False, 6, 2), (4, True, 3, 3), (5, False, 7, 4),
+                                                   (7, True, 6, 5), (6, True, 4, 6)])
+def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed):
+    """The coordinator over 1-7 cache groups (buckets of up to three), none
+    and align mode, shuffled request rows: plan, folded pages, conv states and
+    the align publication against the oracle, group by group."""
+    gen = torch.Generator().manual_seed(seed)
+    request_rows = torch.randperm(B, generator=gen).tolist()
+    sampled = torch.randint(0, 5, (B,), generator=gen, dtype=torch.int32)
+    groups = [_group(B, 2, 4, 64, 64, 4, 1 + g % 2, align=align, seed=400 + 10 * seed + g, page_offset=3 * g)
+              for g in range(n_groups)]
+    for G in groups[1:]:
+        G["qsl"] = groups[0]["qsl"].clone()
+        if align:
+            G["C"] = groups[0]["C"].clone()
+    metas, devs = [], []
+    for G in groups:
+        if align:
+            C = G["C"].long()
+            src_col = torch.clamp(C - 1, min=0) // G["Bk"]
+            table = torch.zeros_like(G["table"])
+            for r in range(B):
+                for j in range(3):
+                    table[r, int(src_col[r]) + j] = 1 + 3 * r + j
+            G["table"], G["src"] = table, table[torch.arange(B), src_col].clone()
+        _index_by_request(G, request_rows)
+        ckpts, convs, recs = _to_dev(G, dev)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+        devs.append((ckpts, convs))
+        metas.append(_entry(G, ctx, dev, request_rows).metadata)
+    mapping = torch.randperm(B + 2, generator=gen)[:B].to(torch.int32)
+    mapping[0] = -1
+    cols = torch.full((B + 2,), -9, dtype=torch.int32)
+    accp = torch.full((B + 2,), 7, dtype=torch.int32)
+    cols_d, accp_d = cols.to(dev), accp.to(dev)
+    print(f"coordinator: {n_groups} groups align={align} B={B} requests={request_rows}", flush=True)
+    coord = GroupedCommitCoordinator()
+    coord.commit(metas, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
+    torch.cuda.synchronize()
+    buckets = -(-n_groups // 3)
+    assert coord.last_group_count == n_groups
+    assert coord.last_launch_count == 2 * buckets + (1 if align and buckets > 1 else 0)
+    want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, align, B)
+    if align:
+        assert cols_d.cpu().tolist() == want["persistent_cols"].tolist()
+        assert accp_d.cpu().tolist() == want["persistent_accepted"].tolist()
+    for gi, G in enumerate(groups):
+        seg = slice(gi * B, gi * B + B)
+        corrs, keys, decays = _planes(G)
+        wstate = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=want["source"][seg], lengths=want["length"][seg],
+                               final=want["final"][seg], boundary=want["boundary"][seg],
+                               boundary_len=want["boundary_len"][seg], rows=B, num_blocks=G["NB"], record_rows=B)
+        targeted = set(want["final"][seg].tolist()) | set(want["boundary"][seg].tolist())
+        _check_states(devs[gi][0], wstate, torch.float32, targeted)
+        wconv = O.oracle_conv_compact(G["convs"], source=want["source"][seg], lengths=want["length"][seg],
+                                      final=want["final"][seg], boundary=want["boundary"][seg],
+                                      boundary_len=want["boundary_len"][seg], history=HIST, num_blocks=G["NB"],
+                                      rows=B, align=align)
+        for li, (got, w) in enumerate(zip(devs[gi][1], wconv)):
+            assert torch.equal(got.cpu(), w), f"group {gi} layer {li}: conv states differ"
+    assert int(want["length"].gt(0).sum()) > 0
