@@ -4,14 +4,23 @@ built and checked against the loaded library without a single launch, and
 the prepared grouped bucket is adopted by the first real commit.
 """
 
+import json
+import os
 from types import SimpleNamespace
 
 import pytest
 import torch
 
 from gdn_recoverssm_ascend import kernels as Kmod
-from gdn_recoverssm_ascend.grouped_commit import GroupedCommitCoordinator, prepare_grouped_commit
-from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers
+from gdn_recoverssm_ascend.grouped_commit import (
+    CommitEntry,
+    GroupedCommitBucket,
+    GroupedCommitCoordinator,
+    prepare_grouped_commit,
+)
+from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_known_answers.json")
 
 pytestmark = pytest.mark.gpu
 
@@ -103,3 +112,50 @@ def test_prepare_grouped_commit_is_adopted_by_the_coordinator(dev):
                                                     id(builders[3]._prepared_group_bucket)}
     assert coord.last_launch_count == 4
     assert all(torch.equal(a, b) for a, b in zip(pages, [p for c in contexts for p in c.checkpoints]))
+
+
+def test_native_config_prefixes_match_reference(dev):
+    """The verify and fold configs the host layer builds for the launch setups
+    of the reference's backend tests (tests/test_ascendc_backend.py:38-77 and
+    :118-168): field prefixes, the column-view index stride and the default
+    scale, built without a launch."""
+    gold = json.load(open(GOLDEN))["native_config_prefixes"]
+    bf = torch.bfloat16
+    q = torch.zeros((1, 8, 1, 128), dtype=bf, device=dev)
+    value = torch.zeros((1, 8, 3, 128), dtype=bf, device=dev)
+    record = ReplayRecordBuffers.allocate(2, 3, 1, 4, 128, 128, device=dev, key_dtype=bf)
+    specs = []
+    before = _launches()
+    gdn_recoverssm_verify(torch.zeros((1, 8, 3), device=dev), torch.zeros((1, 8, 3), device=dev), q, q.clone(), value,
+                          checkpoint_state=torch.zeros((4, 3, 128, 128), device=dev), replay_cache=record,
+                          query_start_loc=torch.tensor([0, 4, 8], dtype=torch.int32, device=dev),
+                          state_indices=torch.ones((2, 4), dtype=torch.int32, device=dev)[:, 0], spec_query_len=4,
+                          _collect=specs)
+    cfg = specs[0].config
+    assert len(cfg) == 28
+    assert list(cfg[:8]) == gold["verify_prefix"]
+    assert cfg[-1] == gold["verify_index_stride_column_view"]
+    assert specs[0].scale == pytest.approx(128 ** -0.5)
+
+    contexts = []
+    for _ in range(2):
+        rec = ReplayRecordBuffers.allocate(2, 3, 1, 4, 128, 128, device=dev, key_dtype=bf)
+        contexts.append(GDNRecoverSSMCommitContext.from_tensors(
+            [torch.zeros((4, 8, 6), device=dev)], [torch.zeros((4, 3, 128, 128), device=dev)], [rec],
+            spec_query_len=4, max_num_reqs=2))
+    entries = []
+    for ctx in contexts:
+        p = SimpleNamespace(
+            state_indices=torch.tensor([1, 2], dtype=torch.int32, device=dev),
+            query_start_loc=torch.tensor([0, 4, 8], dtype=torch.int32, device=dev),
+            request_indices=torch.tensor([0, 1], dtype=torch.int64, device=dev),
+            block_table=None, num_computed_tokens=None, block_size=None, request_rows=(0, 1), query_lens=(4, 4),
+        )
+        entries.append(CommitEntry(None, p, ctx))
+    bucket = GroupedCommitBucket(tuple(contexts))
+    persistent = torch.zeros(2, dtype=torch.int32, device=dev)
+    fold = bucket.make_specs(entries, torch.ones(2, dtype=torch.int32, device=dev), persistent.clone(),
+                             persistent.clone(), persistent.clone(), fuse_plan_fold=False)[-1]
+    assert fold.name == "fold" and len(fold.config) == 17
+    assert list(fold.config[:9]) == gold["fold_prefix"]
+    assert _launches() == before
