@@ -471,17 +471,23 @@ def test_random_configurations(dev, case):
         assert torch.equal(got.cpu(), w), f"layer {li}: conv states differ"
 
 
-@pytest.mark.parametrize("n_groups,align,B,seed", [(1, True, 5, 1), (2, False, 6, 2), (4, True, 3, 3), (5, False, 7, 4),
-                                                   (7, True, 6, 5), (6, True, 4, 6)])
-def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed):
+@pytest.mark.parametrize("n_groups,align,B,seed,hetero", [
+    (1, True, 5, 1, False), (2, False, 6, 2, False), (4, True, 3, 3, False), (5, False, 7, 4, False),
+    (7, True, 6, 5, False), (6, True, 4, 6, False), (4, True, 5, 7, True), (3, False, 4, 8, True),
+])
+def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed, hetero):
     """The coordinator over 1-7 cache groups (buckets of up to three), none
-    and align mode, shuffled request rows: plan, folded pages, conv states and
-    the align publication against the oracle, group by group."""
+    and align mode, shuffled request rows, and (hetero) groups of two record
+    layouts that land in separate buckets (FP32 keys in every other group):
+    plan, folded pages, conv states and the align publication, which must wait
+    for every bucket, against the oracle group by group; a second commit of
+    the same groups reuses the buckets (grouped_commit.py:955-1002)."""
     gen = torch.Generator().manual_seed(seed)
     request_rows = torch.randperm(B, generator=gen).tolist()
     sampled = torch.randint(0, 5, (B,), generator=gen, dtype=torch.int32)
-    groups = [_group(B, 2, 4, 64, 64, 4, 1 + g % 2, align=align, seed=400 + 10 * seed + g, page_offset=3 * g)
-              for g in range(n_groups)]
+    key_dtypes = [torch.float32 if hetero and g % 2 else torch.bfloat16 for g in range(n_groups)]
+    groups = [_group(B, 2, 4, 64, 64, 4, 1 + g % 2, align=align, seed=400 + 10 * seed + g, page_offset=3 * g,
+                     key_dtype=key_dtypes[g]) for g in range(n_groups)]
     for G in groups[1:]:
         G["qsl"] = groups[0]["qsl"].clone()
         if align:
@@ -510,8 +516,9 @@ def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed):
     coord = GroupedCommitCoordinator()
     coord.commit(metas, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
     torch.cuda.synchronize()
-    buckets = -(-n_groups // 3)
-    assert coord.last_group_count == n_groups
+    n_fp32 = sum(dt == torch.float32 for dt in key_dtypes)
+    buckets = -(-(n_groups - n_fp32) // 3) + -(-n_fp32 // 3)
+    assert coord.last_group_count == n_groups and len(coord._buckets) == buckets
     assert coord.last_launch_count == 2 * buckets + (1 if align and buckets > 1 else 0)
     want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, align, B)
     if align:
@@ -532,3 +539,9 @@ def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed):
         for li, (got, w) in enumerate(zip(devs[gi][1], wconv)):
             assert torch.equal(got.cpu(), w), f"group {gi} layer {li}: conv states differ"
     assert int(want["length"].gt(0).sum()) > 0
+    # the same groups again: same buckets, no new epoch
+    first = dict(coord._buckets)
+    coord.commit(metas, torch.zeros(B, dtype=torch.int32, device=dev), mapping.to(dev), cols_d, accp_d)
+    torch.cuda.synchronize()
+    assert coord._buckets.keys() == first.keys()
+    assert all(coord._buckets[k] is first[k] for k in first)

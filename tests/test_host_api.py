@@ -89,6 +89,9 @@ def _verify_inputs(dtype=torch.bfloat16):
         (lambda d: d.update(state_indices=torch.tensor([[1, 2]], dtype=torch.int32)), "one-dimensional"),
         (lambda d: d.update(query_start_loc=torch.tensor([0, 4, 8, 12], dtype=torch.int32),
                             state_indices=torch.tensor([1], dtype=torch.int32)), "query metadata is incompatible"),
+        # lossy key records (tests/test_record_buffers.py:193-222 of the reference)
+        (lambda d: d.update(qk_already_normalized=False), "already-normalized"),
+        (lambda d: d.update(q=d["q"].half(), k=d["k"].half(), v=d["v"].half()), "already-normalized"),
         (lambda d: None, "HIP device"),  # well-formed, but there is no CPU path
     ],
 )
