@@ -1,6 +1,7 @@
 """One whole speculative step at the full sizes of the benchmark configurations
 (B=64 from a 512-page pool, B=256 align mode with boundary crossings and
-padded rows, B=256 plain decode at Q=1, B=256 at Q=8 with skewed acceptance):
+padded rows, B=256 plain decode at Q=1, B=256 at Q=8 with skewed acceptance)
+and at two extremes (2048 rows of small heads; K=256, V=1024 at Q=8):
 verify over every row, then the commit (plan + fold in one launch, conv
 compaction), against the CPU oracle run over every row on the same inputs.
 
@@ -25,9 +26,20 @@ def dev(gpu_device):
     return gpu_device
 
 
-@pytest.mark.parametrize("name", ["pool512_b64", "align_b256", "decode_q1_b256", "skewed_q8_b256"])
+EXTREMES = {
+    # many rows with small heads: 2048 rows, 2 value heads of 32 x 32, Q=2
+    "rows_2048": ("pool512_b64", dict(rows=2048, key_heads=1, value_heads=2, key_dim=32, value_dim=32, window=2,
+                                      pool_pages=2100)),
+    # the largest heads the kernels take: K=256, V=1024 (eight verify tiles), Q=8, align mode
+    "k256_v1024_q8": ("align_b256", dict(rows=3, key_heads=1, value_heads=2, key_dim=256, value_dim=1024, window=8,
+                                         padded_rows=0, crossing_fraction=1.0)),
+}
+
+
+@pytest.mark.parametrize("name", ["pool512_b64", "align_b256", "decode_q1_b256", "skewed_q8_b256", *EXTREMES])
 def test_full_step_against_oracle(dev, name):
-    w = W.make_workload(name, gen_device=dev.type)
+    base, over = EXTREMES.get(name, (name, {}))
+    w = W.make_workload(base, gen_device=dev.type, **over)
     s = w.spec
     B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
     align = w.meta.block_table is not None
