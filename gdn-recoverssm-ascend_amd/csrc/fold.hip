@@ -167,11 +167,6 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
     float h[ITERS][E];
 #pragma unroll
     for (int i = 0; i < ITERS; ++i) unpack16<S>(raw[i], h[i]);
-    // raw is written again only by the next batch's loads, after h is stored:
-    // ending its live range here lets h reuse its registers (FP32 state: 99
-    // instead of 162 VGPRs, four workgroups per CU instead of three).
-#pragma unroll
-    for (int i = 0; i < ITERS; ++i) raw[i] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       if (t < n) {
