@@ -90,7 +90,8 @@ typedef struct gdn_fold_ext {
 
 int gdn_recoverssm_abi_version(void);
 
-/* Last error message of the calling thread ("" when none). */
+/* Message of the calling thread's last failed call ("" before any failure); a
+ * successful call leaves it unchanged, so read it only after a non-zero status. */
 const char *gdn_recoverssm_last_error(void);
 
 /* Speculative verify from the read-only checkpoint (kernels.py:491-697).
