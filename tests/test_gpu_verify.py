@@ -347,3 +347,33 @@ def test_random_configurations(dev, case):
                  state_dtype=p["state_dtype"], null_rows=p["null_rows"], oob_rows=p["oob_rows"],
                  normalise=p["normalise"])
     _run_and_check(P, dev, **c["run"])
+
+
+def test_launches_follow_the_current_stream(dev):
+    """Every launch goes on torch's current stream (csrc/ops.cpp:142-153 of the
+    reference runs on the device's current stream): a verify issued inside
+    ``torch.cuda.stream(s)`` behind a spin kernel on s is still pending on s
+    after the default stream has drained, and then matches the same verify
+    run on the default stream."""
+    P = _problem(4, 2, 4, 128, 128, 4, seed=77)
+    inp, B, H, HV, K, V, Q, T = P["inp"], P["B"], P["H"], P["HV"], P["K"], P["V"], P["Q"], P["T"]
+    args = (inp.g.to(dev), inp.beta.to(dev), inp.q.to(dev), inp.k.to(dev), inp.v.to(dev))
+    kw = dict(checkpoint_state=P["ckpt"].to(dev), query_start_loc=P["qsl"].to(dev),
+              state_indices=P["idx"].to(dev), spec_query_len=Q)
+    outs = []
+    for side in (False, True):
+        rec = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype)
+        torch.cuda.synchronize()
+        if side:
+            s = torch.cuda.Stream(device=dev)
+            with torch.cuda.stream(s):
+                torch.cuda._sleep(20_000_000)
+                out = gdn_recoverssm_verify(*args, replay_cache=rec, **kw)
+            torch.cuda.default_stream(dev).synchronize()
+            assert not s.query(), "the verify did not queue behind the side stream's spin kernel"
+            s.synchronize()
+        else:
+            out = gdn_recoverssm_verify(*args, replay_cache=rec, **kw)
+            torch.cuda.synchronize()
+        outs.append((out.clone(), rec.correction.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
