@@ -143,3 +143,54 @@ def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act):
     for li, (x, y) in enumerate(zip(ref_convs, got_convs)):
         assert torch.equal(x, y), f"layer {li}: conv states differ"
     assert sum(int((h["plan"][0] > 0).sum()) for h in ref) > 0
+
+
+def test_deferred_commit_with_reordered_rows(dev):
+    """The next step's batch lists the rows in another order: the pending
+    commit's arrays are indexed by the next step's row and ``rows`` points at
+    the record row the pending step wrote (row b of the new batch is old row
+    perm[b]). Outputs, records and folded pages equal the ordinary flow's."""
+    from gdn_recoverssm_ascend.kernels import PendingCommit
+
+    w = W.make_workload("decode_loop_l48", layers=1, rows=8, key_heads=2, value_heads=4, steps=2, max_position=256,
+                        block_size=8, padded_rows=1, seed=21)
+    s = w.spec
+    B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+    gen = torch.Generator().manual_seed(22)
+    acc0 = W.sample_accepted(s, B, gen)
+    perm = torch.randperm(B, generator=gen)
+    wd = w.to(dev)
+    inp, m = wd.inputs[0], wd.meta
+    kw = dict(block_table=m.block_table, num_computed_tokens=m.num_computed, mamba_block_size=s.block_size)
+    results = []
+    for deferred in (False, True):
+        ckpt, conv = wd.checkpoints[0].clone(), wd.conv_states[0].clone()
+        recs = [ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype) for _ in range(2)]
+        ctx = GDNRecoverSSMCommitContext.from_tensors([conv], [ckpt], [recs[0]], spec_query_len=Q, max_num_reqs=B)
+        idx0 = m.state_indices.clone()
+        args = (inp.g, inp.beta, inp.q, inp.k, inp.v)
+        gdn_recoverssm_verify(*args, checkpoint_state=ckpt, replay_cache=recs[0], query_start_loc=m.query_start_loc,
+                              state_indices=idx0, spec_query_len=Q)
+        if deferred:
+            pend = ctx.commit_deferred(acc0.to(dev), idx0, m.query_start_loc, **kw)[0]
+        else:
+            ctx.commit(acc0.to(dev), idx0, m.query_start_loc, **kw)
+        lens = ctx.commit_lens[:B]
+        idx1 = torch.where(lens > 0, ctx.final_state_indices[:B], idx0)[perm.to(dev)].contiguous()
+        kw1 = dict(checkpoint_state=ckpt, replay_cache=recs[1], query_start_loc=m.query_start_loc,
+                   state_indices=idx1, spec_query_len=Q)
+        if deferred:
+            p = perm.to(dev)
+            moved = PendingCommit(pend.rows[p].contiguous(), pend.source[p].contiguous(), pend.lengths[p].contiguous(),
+                                  pend.final[p].contiguous(), pend.boundary[p].contiguous(),
+                                  pend.boundary_len[p].contiguous(), pend.records)
+            out = gdn_recoverssm_verify_deferred(*args, pending=moved, **kw1)
+        else:
+            out = gdn_recoverssm_verify(*args, **kw1)
+        torch.cuda.synchronize()
+        results.append([out.clone(), recs[1].correction.clone(), recs[1].key.clone(), recs[1].decay.clone(),
+                        ckpt.clone()])
+        if not deferred:
+            assert int((lens > 0).sum()) > 0 and not torch.equal(perm, torch.arange(B))
+    for name, a, b in zip(("out", "correction", "key", "decay", "pages"), *results):
+        assert torch.equal(a, b), f"{name} differs"
