@@ -545,3 +545,35 @@ def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed, hetero
     torch.cuda.synchronize()
     assert coord._buckets.keys() == first.keys()
     assert all(coord._buckets[k] is first[k] for k in first)
+
+
+@pytest.mark.parametrize("align", [False, True])
+def test_commit_int64_metadata(dev, align):
+    """int64 accepted counts, state indices (a column view of a wider table),
+    query offsets, request mapping, block table and computed-token counts:
+    the same plan, pages and conv states as the oracle."""
+    B = 9
+    G = _group(B, 2, 4, 128, 128, 4, 1, align=align, seed=55 + align, qlens=[4] * 7 + [3, 0])
+    ckpts, convs, recs = _to_dev(G, dev)
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+    table64 = torch.zeros(B, 5, dtype=torch.int64, device=dev)
+    table64[:, 0] = G["src"].to(dev).long()
+    i64 = lambda t: None if t is None else t.long().to(dev)  # noqa: E731
+    ctx.commit(i64(G["acc"]), table64[:, 0], i64(G["qsl"]), request_indices=torch.arange(B, device=dev),
+               block_table=i64(G["table"]), num_computed_tokens=i64(G["C"]), mamba_block_size=G["Bk"])
+    torch.cuda.synchronize()
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=4, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    for key, t in (("commit_lens", ctx.commit_lens), ("final", ctx.final_state_indices),
+                   ("boundary", ctx.boundary_state_indices), ("boundary_len", ctx.boundary_recovery_lens)):
+        assert t[:B].cpu().tolist() == plan[key].tolist(), f"plan {key} differs"
+    corrs, keys, decays = _planes(G)
+    want = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=G["src"], lengths=plan["commit_lens"],
+                         final=plan["final"], boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                         rows=B, num_blocks=G["NB"], record_rows=B)
+    _check_states(ckpts, want, torch.float32, set(plan["final"].tolist()) | set(plan["boundary"].tolist()))
+    want_conv = O.oracle_conv_compact(G["convs"], source=G["src"], lengths=plan["commit_lens"], final=plan["final"],
+                                      boundary=plan["boundary"], boundary_len=plan["boundary_len"], history=HIST,
+                                      num_blocks=G["NB"], rows=B, align=align)
+    assert torch.equal(convs[0].cpu(), want_conv[0])
+    assert int(plan["commit_lens"].gt(0).sum()) > 0
