@@ -629,6 +629,44 @@ def main():
         }
     gbs = total / (step_ms * 1e-3) / 1e9
     others = None if args.kernel_only else other_configs(args, timer, s.name)
+
+    # The same step with packed FP32 records, one [corr(V) | key(K) | decay]
+    # row per (row, value head, token) (kernels.py:687-697), instead of the
+    # typed planes with bf16 keys shared by a key head's value heads.
+    packed = None
+    if not args.kernel_only:
+        prec = torch.zeros(B, HV, Q, V + K + 1, dtype=torch.float32, device=dev)
+        pctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, [prec], spec_query_len=Q,
+                                                       max_num_reqs=B)
+        pspecs: list = []
+        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0],
+                              replay_cache=prec, query_start_loc=m.query_start_loc, state_indices=m.state_indices,
+                              spec_query_len=Q, out=out, _collect=pspecs)
+        pspecs += list(pctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc, commit_conv=False,
+                                              **align_kw))
+        for _ in range(args.warmup):
+            for sp in pspecs:
+                sp.launch()
+        p0, p1 = timer.event(), timer.event()
+        torch.cuda.synchronize()
+        timer.record(p0)
+        for _ in range(args.steps):
+            for sp in pspecs:
+                sp.launch()
+        timer.record(p1)
+        torch.cuda.synchronize()
+        pms = timer.elapsed(p0, p1) / args.steps
+        T_, acc_ = nbytes["tokens"], nbytes["accepted_tokens"]
+        typed_rec, packed_rec = HV * V * 4 + H * K * 2 + HV * 4, HV * (V + K + 1) * 4
+        pbytes = total + (T_ + acc_) * (packed_rec - typed_rec)
+        packed = {
+            "us_per_step": round(pms * 1e3, 2),
+            "bytes": pbytes,
+            "gbs": round(pbytes / (pms * 1e-3) / 1e9, 1),
+            "frac": round(pbytes / (pms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "verify + plan_fold with packed FP32 records [corr|key|decay] per value head; bytes = the typed "
+                    "step's with each written and each folded token's record at (V+K+1)*4 per value head",
+        }
     full_step = None
     if full_ms is not None:
         conv_dim, conv_len = w.conv_states[0].shape[1:]
@@ -717,6 +755,7 @@ def main():
         "cpu_baseline": cpu,
         "fused_gating": fused,
         "with_conv_compaction": full_step,
+        "packed_records": packed,
         "deferred_commit": deferred,
         "other_configs": others,
     }
