@@ -163,3 +163,29 @@ def test_native_caller_is_built_against_this_header():
         pytest.skip("tests/capi/capi_step is built by __graft_entry__.build()")
     r = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=60)
     assert r.returncode == 2 and b"usage" in r.stdout
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """With the HIP library absent, the first call into the package raises
+    RuntimeError naming the missing path: there is no CPU fallback to fall
+    through to. Run in a child process, since the library loads once per
+    process."""
+    code = (
+        "import torch\n"
+        "from gdn_recoverssm_ascend import torch_ops, _native\n"
+        "for call in (torch.ops.gdn_recoverssm_hip.abi_version, _native.load):\n"
+        "    try:\n"
+        "        call()\n"
+        "    except RuntimeError as e:\n"
+        "        assert 'not found' in str(e) and 'no fallback' in str(e), str(e)\n"
+        "    else:\n"
+        "        raise SystemExit('no error without the library')\n"
+        "print('ok')\n"
+    )
+    pkg = os.path.dirname(os.path.dirname(N.__file__))
+    env = dict(os.environ, GDN_RECOVERSSM_HIP_LIB=str(tmp_path / "absent.so"),
+               PYTHONPATH=pkg + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    r = subprocess.run(["python3", "-c", code], env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       timeout=300)
+    out = r.stdout.decode(errors="replace")
+    assert r.returncode == 0 and out.strip().endswith("ok"), out
