@@ -223,6 +223,22 @@ def test_publish_across_buckets_requires_all_valid_and_agreeing_columns():
     assert c.tolist() == [-9, 2, -9, -9] and a.tolist() == [7, 1, 7, 7]
 
 
+def test_publish_maps_committed_rows_to_slots():
+    """Only committed rows are published, each at its idx_mapping slot; a row
+    whose request maps to -1 and every other slot keep their values. Row 1 is
+    a valid plan row here, so the -1 mapping alone must skip it."""
+    sm = GOLD["publication_slot_mapping"]
+    rows = len(sm["idx_mapping"])
+    valid = torch.ones(rows, dtype=torch.int32)
+    col = torch.full((rows,), 5, dtype=torch.int32)
+    for r, c in zip(sm["committed_rows"], sm["committed_cols"]):
+        col[r] = c
+    init = torch.full((sm["slots"],), sm["initial"], dtype=torch.int32)
+    c, a = O.oracle_publish([(valid, col, rows, 1)], torch.arange(rows), torch.tensor(sm["idx_mapping"]),
+                            init, init.clone(), rows=rows)
+    assert c.tolist() == sm["expected_cols"] and a.tolist() == sm["expected_accepted"]
+
+
 def test_conv_compaction_index_identity():
     hist, Q = 3, 4
     window = hist + Q - 1
