@@ -42,7 +42,10 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps before the timed ones (default: 200 for a single-layer step, whose "
+                         "timed steps ran 2 us slower each after only 10; 10 for a decode loop, which carries "
+                         "its state through them)")
     ap.add_argument("--workload", default="align_b256")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--deferred", action="store_true",
@@ -437,7 +440,11 @@ def main():
     from gdn_recoverssm_ascend import workloads as W
 
     if W.get_spec(args.workload).layers > 1:
+        if args.warmup is None:
+            args.warmup = 10
         return decode_loop(args)
+    if args.warmup is None:
+        args.warmup = 200
     import torch
 
     from gdn_recoverssm_ascend import workloads as W
