@@ -6,6 +6,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 import tempfile
 
 import pytest
@@ -185,7 +186,7 @@ def test_missing_library_fails_loudly(tmp_path):
     pkg = os.path.dirname(os.path.dirname(N.__file__))
     env = dict(os.environ, GDN_RECOVERSSM_HIP_LIB=str(tmp_path / "absent.so"),
                PYTHONPATH=pkg + os.pathsep + os.environ.get("PYTHONPATH", ""))
-    r = subprocess.run(["python3", "-c", code], env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+    r = subprocess.run([sys.executable, "-c", code], env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                        timeout=300)
     out = r.stdout.decode(errors="replace")
     assert r.returncode == 0 and out.strip().endswith("ok"), out
