@@ -259,12 +259,13 @@ def conv_bytes(spec, n, bnd, blen, num_pages, conv_dim, history, elem):
     return (int(active.sum()) * 2 + int(store_b.sum()) * 2) * conv_dim * history * elem
 
 
-def decode_loop(args):
+def run_decode_loop(name, *, deferred, steps=None, warmup=10):
     """The decode-loop workload: every layer's verify, then one commit (plan,
     conv compaction, fold) across all layers, per speculative step, with the
     state carried from step to step (C += n, the source page becomes the final
-    page) and fresh accepted lengths each step. With --deferred each step runs
-    the verify that applies the previous step's fold, then plan + conv."""
+    page) and fresh accepted lengths each step. With ``deferred`` each step runs
+    the verify that applies the previous step's fold, then plan + conv.
+    Returns the loop's JSON line as a dict."""
     import torch
 
     from gdn_recoverssm_ascend import workloads as W
@@ -277,12 +278,12 @@ def decode_loop(args):
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    w = W.make_workload(args.workload, gen_device="cuda").to(dev)
+    w = W.make_workload(name, gen_device="cuda").to(dev)
     s = w.spec
     L, B, Q, H, HV, K, V = s.layers, s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
-    steps = s.steps if args.loop_steps is None else args.loop_steps
+    steps = s.steps if steps is None else steps
     m = w.meta
-    sets = 2 if args.deferred else 1
+    sets = 2 if deferred else 1
     recs = [[ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=w.inputs[0].k.dtype)
              for _ in range(L)] for _ in range(sets)]
     ctxs = [GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, recs[i], spec_query_len=Q,
@@ -291,14 +292,14 @@ def decode_loop(args):
     computed = m.num_computed.clone()
     accepted = torch.zeros(B, dtype=torch.int32, device=dev)
     gen = torch.Generator().manual_seed(7)
-    acc_all = torch.stack([W.sample_accepted(s, B, gen) for _ in range(steps + args.warmup)]).to(dev)
+    acc_all = torch.stack([W.sample_accepted(s, B, gen) for _ in range(steps + warmup)]).to(dev)
     outs = [torch.empty(1, w.tokens, HV, V, dtype=w.inputs[0].v.dtype, device=dev) for _ in range(L)]
     commit_kw = dict(block_table=m.block_table, num_computed_tokens=computed, mamba_block_size=m.block_size,
                      commit_conv=True)
     cspecs, pendings = [], []
     for i in range(sets):
         specs_i: list = []
-        if args.deferred:
+        if deferred:
             pendings.append(ctxs[i].commit_deferred(accepted, state_idx, m.query_start_loc, _collect=specs_i,
                                                     **commit_kw))
         else:
@@ -312,7 +313,7 @@ def decode_loop(args):
             kw = dict(checkpoint_state=w.checkpoints[layer], replay_cache=recs[i][layer],
                       query_start_loc=m.query_start_loc, state_indices=state_idx, spec_query_len=Q, out=outs[layer],
                       _collect=specs_i)
-            if args.deferred:
+            if deferred:
                 gdn_recoverssm_verify_deferred(inp.g, inp.beta, inp.q, inp.k, inp.v,
                                                pending=pendings[1 - i][layer], **kw)
             else:
@@ -356,7 +357,7 @@ def decode_loop(args):
     timer = _HipTimer(stream.cuda_stream)
     start_idx, start_c = state_idx.clone(), computed.clone()
     restart()
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(steps + i)
     torch.cuda.synchronize()
     restart()
@@ -395,15 +396,15 @@ def decode_loop(args):
     step_ms = total_ms / steps
     total_b = verify_b * steps + commit_b + conv_b
     gbs = total_b / (total_ms * 1e-3) / 1e9
-    mode = "deferred commit (fold applied by the next verify)" if args.deferred else "verify then commit"
+    mode = "deferred commit (fold applied by the next verify)" if deferred else "verify then commit"
     line = {
         "metric": f"decode loop: {L} GDN layers verify + one grouped commit per step, B={B} Q={Q}, state carried"
-                  + (", deferred commit" if args.deferred else ""),
+                  + (", deferred commit" if deferred else ""),
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(step_ms, 4),
         "us_per_step": round(step_ms * 1e3, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -419,15 +420,55 @@ def decode_loop(args):
         "tokens_committed_per_step": round(tokens_committed / steps, 1),
         "mode": mode,
     }
-    if args.deferred:
+    if deferred:
         # The step's state reads that the deferred commit removes: one page read
         # per committed (row, layer).
         saved = sum(int((hist_lens[i, 0] > 0).sum()) for i in range(steps)) * L * HV * V * K * 4
         line["hbm_bytes_per_step"] = round((total_b - saved) / steps)
         line["hbm_gbs"] = round((total_b - saved) / (total_ms * 1e-3) / 1e9, 1)
         line["note"] = "value divides the ordinary flow's algorithmic bytes by this loop's time"
+    del w, recs, ctxs, outs, cspecs, vspecs, pendings
+    torch.cuda.empty_cache()
+    return line
+
+
+def decode_loop(args):
+    """--workload decode_loop_l48 [--deferred]: the loop's own JSON line."""
+    line = run_decode_loop(args.workload, deferred=args.deferred, steps=args.loop_steps, warmup=args.warmup)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def decode_loop_summary(warmup):
+    """The decode-loop configuration (48 layers, B=128, Q=4, align, 64 carried
+    steps) for the default bench line: per-step time, sustained bandwidth and
+    the phase split, verify then commit and with the deferred commit."""
+    keys = ("us_per_step", "value", "hbm_frac", "steps", "warmup", "phases_us_per_step", "bytes_per_step",
+            "tokens_committed_per_step")
+    res = {}
+    for mode, deferred in (("ordinary", False), ("deferred", True)):
+        line = run_decode_loop("decode_loop_l48", deferred=deferred, warmup=warmup)
+        entry = {k: line[k] for k in keys}
+        entry["gbs"] = entry.pop("value")
+        if deferred:
+            entry["equivalent_gbs"] = entry.pop("gbs")
+            entry["equivalent_frac"] = entry.pop("hbm_frac")
+            entry["hbm_bytes_per_step"] = line["hbm_bytes_per_step"]
+            entry["hbm_gbs"] = line["hbm_gbs"]
+        res[mode] = entry
+    res["config"] = run_decode_loop_config()
+    res["note"] = ("gbs = algorithmic bytes of the whole loop (48 verifies, plan + fold, conv compaction per step) / "
+                   "loop time; the deferred flow's equivalent_gbs divides the ordinary flow's bytes by its time")
+    return res
+
+
+def run_decode_loop_config():
+    from gdn_recoverssm_ascend import workloads as W
+
+    s = W.get_spec("decode_loop_l48")
+    return {"workload": s.name, "layers": s.layers, "rows": s.rows, "key_heads": s.key_heads,
+            "value_heads": s.value_heads, "key_dim": s.key_dim, "value_dim": s.value_dim, "window": s.window,
+            "mode": "align", "block_size": s.block_size, "steps": s.steps}
 
 
 def main():
@@ -596,11 +637,18 @@ def main():
             pend[i] = ctx2[i].commit_deferred(m.accepted, m.state_indices, m.query_start_loc, _collect=specs_i,
                                               **commit_kw)
             dspecs[i] = specs_i
+        # Each step plans the same commit (source pages -> final pages); the
+        # verify that applies it names each committed row's final page, as a
+        # carried batch does, so every pending fold is applied.
+        for sp in dspecs[0]:
+            sp.launch()
+        idx_next = torch.where(ctx2[0].commit_lens[:B] > 0, ctx2[0].final_state_indices[:B],
+                               m.state_indices).contiguous()
         vdef = [[], []]
         for i in range(2):
             gdn_recoverssm_verify_deferred(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0],
                                            replay_cache=recs2[i], pending=pend[1 - i][0],
-                                           query_start_loc=m.query_start_loc, state_indices=m.state_indices,
+                                           query_start_loc=m.query_start_loc, state_indices=idx_next,
                                            spec_query_len=Q, out=out, _collect=vdef[i])
 
         def dstep(i):
@@ -636,6 +684,9 @@ def main():
         }
     gbs = total / (step_ms * 1e-3) / 1e9
     others = None if args.kernel_only else other_configs(args, timer, s.name)
+    # The 48-layer decode loop at its own size (its own 10 warmup steps, after
+    # which the carried state restarts from the seeded start).
+    loop = None if args.kernel_only else decode_loop_summary(warmup=10)
 
     # The same step with packed FP32 records, one [corr(V) | key(K) | decay]
     # row per (row, value head, token) (kernels.py:687-697), instead of the
@@ -723,12 +774,15 @@ def main():
 
     cpu = None
     if want_cpu:
-        threads = max(1, min(os.cpu_count() or 1, 16))
+        # torch.set_num_threads(os.cpu_count()), whatever share of those CPUs
+        # this process may run on (reported beside it).
+        threads = max(1, os.cpu_count() or 1)
         secs, cpu_steps = cpu_baseline(w_cpu, threads)
         cpu = {
             "value": round(total / secs / 1e9, 3),
             "unit": "GB/s",
             "cores": threads,
+            "cpus_available": len(os.sched_getaffinity(0)),
             "kind": "port",
             "sample": f"{cpu_steps} full verify+plan+fold steps of {s.name} (all {B} rows, the same bytes per step "
                       f"as value) with the FP32 torch oracle, about 10 s of CPU work; {secs * 1e3:.0f} ms/step",
@@ -765,6 +819,7 @@ def main():
         "packed_records": packed,
         "deferred_commit": deferred,
         "other_configs": others,
+        "decode_loop": loop,
     }
     print(json.dumps(line), flush=True)
     return 0

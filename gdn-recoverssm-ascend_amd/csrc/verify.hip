@@ -81,7 +81,7 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     return GDN_ERR_UNSUPPORTED;
   }
   if (pending) {
-    const bool ok = ext->state_dtype == GDN_DT_F32 && pending->record_rows > 0 &&
+    const bool ok = pending->record_rows > 0 && pending->num_rows > 0 && pending->num_rows <= INT32_MAX &&
                     act_or_f32(pending->key_dtype) && fits_i32(pending->corr_strides[1]) &&
                     fits_i32(pending->corr_strides[2]) && fits_i32(pending->key_strides[1]) &&
                     fits_i32(pending->key_strides[2]) && fits_i32(pending->decay_strides[1]) &&
@@ -89,8 +89,8 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
                     (Q - 1) * pending->corr_strides[2] + V < int64_t(kWindowBytes) / 4 &&
                     (Q - 1) * pending->key_strides[2] + K < int64_t(kWindowBytes) / 4;
     if (!ok) {
-      set_error("verify_deferred: FP32 state, FP32 or activation-typed pending keys and 32-bit record strides "
-                "are required");
+      set_error("verify_deferred: a pending plan of at least one row, FP32 or activation-typed pending keys and "
+                "32-bit record strides are required");
       return GDN_ERR_UNSUPPORTED;
     }
   }
@@ -186,6 +186,7 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     a.p_key_f32 = pending->key_dtype == GDN_DT_F32;
     a.p_key_per_value_head = pending->key_per_value_head;
     a.p_record_rows = int32_t(pending->record_rows > 0x7fffffff ? 0x7fffffff : pending->record_rows);
+    a.p_num_rows = int32_t(pending->num_rows);
   }
   if (gating) {
     a.gated = 1;

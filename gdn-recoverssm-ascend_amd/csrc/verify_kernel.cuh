@@ -61,14 +61,15 @@ struct VerifyArgs {
   const void *a_log, *dt_bias;
   int32_t gated, a_log_dt, dt_bias_dt;
   float softplus_beta, softplus_threshold;
-  // Deferred commit (kernels instantiated with DEFER): the previous step's
-  // plan row for every current row and that step's records.
+  // Deferred commit (kernels instantiated with DEFER): for every current row
+  // the pending row it continues (p_rows), the previous step's plan arrays
+  // indexed by pending row, and that step's records.
   const int32_t *p_rows, *p_src, *p_len, *p_final, *p_bnd, *p_blen;
   const float *p_corr, *p_decay;
   const void *p_key;
   int64_t p_corr_rs, p_key_rs, p_decay_rs;
   int32_t p_corr_hs, p_corr_ts, p_key_hs, p_key_ts, p_decay_hs, p_decay_ts;
-  int32_t p_key_f32, p_key_per_value_head, p_record_rows;
+  int32_t p_key_f32, p_key_per_value_head, p_record_rows, p_num_rows;
 };
 
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
@@ -193,8 +194,8 @@ __device__ __forceinline__ int64_t ld_idx(const void *p, int64_t i, bool i64) {
 // from the pending commit's source page, its accepted prefix is replayed from
 // the previous step's records block by block, the result is stored to the
 // final page (and the boundary snapshot to the boundary page), and the window
-// is verified from the folded values. Each state page is read once per step
-// instead of twice. FP32 state only.
+// is verified from the folded values, rounded to the state type exactly as
+// the stored page is. Each state page is read once per step instead of twice.
 template <typename S, typename A, int J, int QM, bool DEFER>
 __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   constexpr int E = Chunk<S>::E;       // elements per 16-byte chunk
@@ -208,7 +209,6 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   __shared__ float d_lds[64][NV + 1];  // GEMV results of one 64-row half tile
   __shared__ float inv_lds[NV];
   __shared__ __align__(16) float pk_lds[DEFER ? QM : 1][DEFER ? KP : 1];  // pending commit's keys
-  static_assert(!DEFER || sizeof(S) == 4, "the deferred commit is built for FP32 state");
 
   const int nvt = a.NVT;
   const int hv = int(blockIdx.x) / nvt;
@@ -228,20 +228,27 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const int64_t out_base = int64_t(hv) * V + row0;
 
   // Pending commit of the previous step (same validity rule as the fold,
-  // kernels.py:1232-1242 / csrc/fold.h:192-205).
+  // kernels.py:1232-1242 / csrc/fold.h:192-205). The row continues pending
+  // row `prow` (plan and record row of the previous step) only when its state
+  // index names that commit's final page: a row whose request is new, or
+  // whose metadata names another page, verifies from its own page and leaves
+  // the pending commit to a flush.
   bool pend = false, pstore_b = false;
   int pn = 0, pblen = 0, prow = 0;
   int64_t psrc = 0, pfin = 0, pbnd = 0;
   if constexpr (DEFER) {
     prow = int(ld_idx(a.p_rows, b, false));
-    pn = int(ld_idx(a.p_len, b, false));
-    psrc = ld_idx(a.p_src, b, false);
-    pfin = ld_idx(a.p_final, b, false);
-    pbnd = ld_idx(a.p_bnd, b, false);
-    pblen = int(ld_idx(a.p_blen, b, false));
-    pend = prow >= 0 && prow < a.p_record_rows && pn > 0 && pn <= Q && psrc > a.null_block && psrc < a.blocks &&
-           pfin > a.null_block && pfin < a.blocks;
+    const bool prow_ok = prow >= 0 && prow < a.p_num_rows && prow < a.p_record_rows;
+    const int pr = prow_ok ? prow : 0;  // p_num_rows >= 1: entry 0 exists
+    pn = int(ld_idx(a.p_len, pr, false));
+    psrc = ld_idx(a.p_src, pr, false);
+    pfin = ld_idx(a.p_final, pr, false);
+    pbnd = ld_idx(a.p_bnd, pr, false);
+    pblen = int(ld_idx(a.p_blen, pr, false));
+    pend = prow_ok && pn > 0 && pn <= Q && psrc > a.null_block && psrc < a.blocks && pfin > a.null_block &&
+           pfin < a.blocks && pfin == slot;
     pstore_b = pend && pbnd > a.null_block && pbnd < a.blocks && pbnd != pfin && pblen > 0 && pblen <= pn;
+    prow = pend ? prow : 0;  // record addressing below stays inside the records
   }
   const int pend_len = pend ? pn : 0;  // tokens of the pending commit to replay
   const bool null_slot = slot <= a.null_block || slot >= a.blocks;
@@ -254,7 +261,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       for (int r = lane; r < TILE; r += kVerifyThreads)
         if (row0 + r < V) st_f32_or<A>(a.out, tok * a.out_ts + out_base + r, a.out_f32 != 0, 0.0f);
     }
-    if (!pend) return;
+    return;  // a pending commit needs slot == its final page, never a null one
   }
   // Token validity is uniform across the wave (kernels.py:612).
   uint32_t valid_mask = 0;
@@ -324,16 +331,20 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   }
   // Gates are wave-uniform: scalar loads of the dword holding each one (FP32,
   // or the 16-bit value at its half), decoded after the state loads issue.
-  // Tokens outside the window read element 0 instead and are discarded.
+  // Tokens outside the window read the first word of query_start_loc instead
+  // (always present; g and beta may be empty, hence null, when the launch has
+  // no token at all) and are discarded.
   const int gsz = a.g_f32 ? 4 : AS, bsz = a.beta_f32 ? 4 : AS;
+  const uintptr_t any_word = reinterpret_cast<uintptr_t>(a.qsl);
   uint32_t graw[QM], braw[QM];
   int gsh[QM], bsh[QM];
 #pragma unroll
   for (int t = 0; t < QM; ++t) {
     const bool tv = (valid_mask >> t) & 1u;
-    const uintptr_t ga = reinterpret_cast<uintptr_t>(a.g) + (tv ? uintptr_t(((bos + t) * a.g_ts + hv) * gsz) : 0);
+    const uintptr_t ga =
+        tv ? reinterpret_cast<uintptr_t>(a.g) + uintptr_t(((bos + t) * a.g_ts + hv) * gsz) : any_word;
     const uintptr_t ba =
-        reinterpret_cast<uintptr_t>(a.beta) + (tv ? uintptr_t(((bos + t) * a.beta_ts + hv) * bsz) : 0);
+        tv ? reinterpret_cast<uintptr_t>(a.beta) + uintptr_t(((bos + t) * a.beta_ts + hv) * bsz) : any_word;
     gsh[t] = int(ga & 2) * 8;
     bsh[t] = int(ba & 2) * 8;
     graw[t] = scalar_word(ga);
@@ -491,6 +502,11 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   auto fold_block = [&](int rb, uint4 (&buf)[J], const float (&pc)[QM]) {
     if constexpr (DEFER) {
       const int seg = pstore_b ? pblen : 0;
+      // FP32 values of the lane's chunks; the fold keeps them in FP32 across
+      // the boundary snapshot and rounds only what it stores, as the fold does.
+      float h[J][E];
+#pragma unroll
+      for (int j = 0; j < J; ++j) unpack16<S>(buf[j], h[j]);
       auto apply = [&](int lo, int hi) {
 #pragma unroll
         for (int t = 0; t < QM; ++t) {
@@ -498,11 +514,14 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
             const float d = pdec[t], c = pc[t];
 #pragma unroll
             for (int j = 0; j < J; ++j) {
-              const float4 kv = *reinterpret_cast<const float4 *>(&pk_lds[t][E * (4 * j + ls)]);
-              buf[j].x = __float_as_uint(__builtin_fmaf(c, kv.x, __uint_as_float(buf[j].x) * d));
-              buf[j].y = __float_as_uint(__builtin_fmaf(c, kv.y, __uint_as_float(buf[j].y) * d));
-              buf[j].z = __float_as_uint(__builtin_fmaf(c, kv.z, __uint_as_float(buf[j].z) * d));
-              buf[j].w = __float_as_uint(__builtin_fmaf(c, kv.w, __uint_as_float(buf[j].w) * d));
+#pragma unroll
+              for (int e4 = 0; e4 < E; e4 += 4) {
+                const float4 kv = *reinterpret_cast<const float4 *>(&pk_lds[t][E * (4 * j + ls) + e4]);
+                h[j][e4 + 0] = __builtin_fmaf(c, kv.x, h[j][e4 + 0] * d);
+                h[j][e4 + 1] = __builtin_fmaf(c, kv.y, h[j][e4 + 1] * d);
+                h[j][e4 + 2] = __builtin_fmaf(c, kv.z, h[j][e4 + 2] * d);
+                h[j][e4 + 3] = __builtin_fmaf(c, kv.w, h[j][e4 + 3] * d);
+              }
             }
           }
         }
@@ -511,14 +530,18 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
           const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, buf[j]),
-                                                 r, vo, rb * 16 * row_bytes, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, pack16<S>(h[j])), r, vo,
+              rb * 16 * row_bytes, 0);
         }
       };
       apply(0, seg);
       store(rbnd);
       apply(seg, pn);
       store(rfin);
+      // The window is verified from the folded tile as stored.
+#pragma unroll
+      for (int j = 0; j < J; ++j) buf[j] = pack16<S>(h[j]);
     }
   };
 
@@ -663,8 +686,7 @@ static void launch_verify_q(int qm, dim3 grid, hipStream_t s, const VerifyArgs &
 }
 
 // J: 16-byte chunks per lane per row, KP = 4 * E * J <= 256, so J <= 16 for
-// f32 state and J <= 8 for 16-bit state. The deferred-commit kernels exist for
-// FP32 state only (the host rejects other state types).
+// f32 state and J <= 8 for 16-bit state.
 template <typename S, typename A, bool DEFER>
 static void launch_verify_j(int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
   switch (j) {
@@ -678,29 +700,35 @@ static void launch_verify_j(int j, int qm, dim3 grid, hipStream_t s, const Verif
   }
 }
 
-// The deferred-commit kernels (FP32 state) live in their own translation unit
-// (verify_f32_deferred.hip) so the two halves compile in parallel.
-void launch_verify_f32_deferred(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a);
-
-template <typename S, typename A>
-static void launch_verify_d(bool deferred, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
-  (void)deferred;
-  launch_verify_j<S, A, false>(j, qm, grid, s, a);
+template <typename S, bool DEFER>
+static void launch_verify_act(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
+  switch (act_dt) {
+    case GDN_DT_BF16: launch_verify_j<S, bf16, DEFER>(j, qm, grid, s, a); break;
+    case GDN_DT_F16: launch_verify_j<S, f16, DEFER>(j, qm, grid, s, a); break;
+    default: launch_verify_j<S, float, DEFER>(j, qm, grid, s, a); break;
+  }
 }
 
-#define GDN_DEFINE_VERIFY_LAUNCH(STATE)                                                                   \
-  template <>                                                                                             \
-  void launch_verify_state<STATE>(int act_dt, int j, int qm, bool deferred, dim3 grid, hipStream_t s,    \
-                                  const VerifyArgs &a) {                                                  \
-    if (deferred) {                                                                                       \
-      launch_verify_f32_deferred(act_dt, j, qm, grid, s, a);                                              \
-      return;                                                                                             \
-    }                                                                                                     \
-    switch (act_dt) {                                                                                     \
-      case GDN_DT_BF16: launch_verify_d<STATE, bf16>(deferred, j, qm, grid, s, a); break;                 \
-      case GDN_DT_F16: launch_verify_d<STATE, f16>(deferred, j, qm, grid, s, a); break;                   \
-      default: launch_verify_d<STATE, float>(deferred, j, qm, grid, s, a); break;                         \
-    }                                                                                                     \
+// The deferred-commit kernels of each state type live in a translation unit of
+// their own (verify_<state>_deferred.hip), so the halves compile in parallel.
+template <typename S>
+void launch_verify_deferred(int act_dt, int j, int qm, dim3 grid, hipStream_t s, const VerifyArgs &a);
+
+#define GDN_DEFINE_VERIFY_LAUNCH(STATE)                                                                \
+  template <>                                                                                          \
+  void launch_verify_state<STATE>(int act_dt, int j, int qm, bool deferred, dim3 grid, hipStream_t s, \
+                                  const VerifyArgs &a) {                                               \
+    if (deferred)                                                                                      \
+      launch_verify_deferred<STATE>(act_dt, j, qm, grid, s, a);                                        \
+    else                                                                                               \
+      launch_verify_act<STATE, false>(act_dt, j, qm, grid, s, a);                                      \
+  }
+
+#define GDN_DEFINE_VERIFY_DEFERRED_LAUNCH(STATE)                                                         \
+  template <>                                                                                            \
+  void launch_verify_deferred<STATE>(int act_dt, int j, int qm, dim3 grid, hipStream_t s,                \
+                                     const VerifyArgs &a) {                                              \
+    launch_verify_act<STATE, true>(act_dt, j, qm, grid, s, a);                                           \
   }
 
 }  // namespace gdn

@@ -19,6 +19,7 @@ from .kernels import (  # noqa: F401
     GDNRecoverSSMCommitContext,
     PendingCommit,
     ReplayRecordBuffers,
+    continue_pending,
     counts,
     gdn_recoverssm_verify,
     gdn_recoverssm_verify_deferred,
@@ -44,6 +45,7 @@ __all__ = [
     "NULL_BLOCK_ID",
     "PendingCommit",
     "ReplayRecordBuffers",
+    "continue_pending",
     "counts",
     "gdn_recoverssm_verify",
     "gdn_recoverssm_verify_deferred",

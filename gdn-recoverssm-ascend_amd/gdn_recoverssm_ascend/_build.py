@@ -68,7 +68,7 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False, jobs: int = min(6, os.cpu_count() or 1)) -> str:
+def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str:
     """Compile every source (in parallel, largest first) and link the shared library."""
     from concurrent.futures import ThreadPoolExecutor
 

@@ -93,6 +93,7 @@ class PendingCommit(ctypes.Structure):
         ("record_rows", c_i64),
         ("corr_strides", c_i64 * 3), ("key_strides", c_i64 * 3), ("decay_strides", c_i64 * 3),
         ("key_dtype", c_i32), ("key_per_value_head", c_i32),
+        ("num_rows", c_i64),
     ]
 
 

@@ -26,7 +26,7 @@ from __future__ import annotations
 import ctypes
 from collections import Counter
 from collections.abc import Sequence
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from typing import Any
 
 import torch
@@ -298,11 +298,18 @@ def gdn_recoverssm_verify_gated(
 class PendingCommit:
     """One layer's commit left for the next verify (``gdn_recoverssm_verify_deferred``).
 
-    Plan arrays are int32 and indexed by the NEXT step's row: ``rows`` is the
-    record row of the pending commit (-1: none), then source page, accepted
-    length, final page, boundary page and boundary length of that commit.
-    ``records`` are the typed records the pending step's verify wrote; the next
-    verify must write a different record buffer.
+    ``rows`` (int32, one entry per row of the next batch) names the pending
+    row each next row continues, -1 for none. The plan arrays (source page,
+    accepted length, final page, boundary page, boundary length; int32) and
+    the records are those of the pending step, indexed by pending row, and
+    cover ``num_rows`` rows. A next row applies its pending commit only when
+    its own state index is that commit's final page; ``records`` are the typed
+    records the pending step's verify wrote, and the next verify must write a
+    different record buffer.
+
+    ``commit_deferred`` returns commits whose ``rows`` continue every row in
+    place (row i of the next batch continues row i); ``continue_pending`` maps
+    a next batch given by request ids instead.
     """
 
     rows: torch.Tensor
@@ -312,6 +319,37 @@ class PendingCommit:
     boundary: torch.Tensor
     boundary_len: torch.Tensor
     records: "ReplayRecordBuffers"
+    num_rows: int = 0
+
+
+def continue_pending(pending: Sequence[PendingCommit], previous_requests: Sequence, next_requests: Sequence):
+    """Re-key one step's pending commits (one per layer) for the next batch.
+
+    ``previous_requests[r]`` identifies the request in row r of the pending
+    step and ``next_requests[b]`` the request in row b of the next batch (any
+    hashable ids, host-side, as the scheduler holds them). Returns the pending
+    commits with a shared row map (next row -> pending row of the same
+    request, -1 for a new request) and the sorted pending rows whose request
+    is not in the next batch: their commits are applied by no verify, so
+    ``flush_deferred(rows=...)`` must fold them before their pages are reused.
+    """
+    _require(len(pending) > 0, "no pending commits to continue")
+    num_rows = int(pending[0].num_rows)
+    _require(all(int(p.num_rows) == num_rows for p in pending), "pending commits of one step disagree on their rows")
+    _require(len(previous_requests) >= num_rows, "previous request ids do not cover the pending rows")
+    where = {}
+    for r, req in enumerate(previous_requests[:num_rows]):
+        _require(req not in where, f"request {req!r} appears twice in the pending step")
+        where[req] = r
+    seen = set()
+    mapping = []
+    for req in next_requests:
+        _require(req not in seen, f"request {req!r} appears twice in the next batch")
+        seen.add(req)
+        mapping.append(where.get(req, -1))
+    left = sorted(r for req, r in where.items() if req not in seen)
+    rows = torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=pending[0].rows.device)
+    return tuple(replace(p, rows=rows) for p in pending), left
 
 
 def gdn_recoverssm_verify_deferred(
@@ -333,14 +371,17 @@ def gdn_recoverssm_verify_deferred(
     _collect: list | None = None,
 ) -> torch.Tensor:
     """Verify with the previous step's commit folded in (the deferred commit of
-    docs/GDN-RecoverSSM-实现方案.md:515-527; FP32 state, typed records).
+    docs/GDN-RecoverSSM-实现方案.md:515-527; typed records).
 
-    For each row with a pending commit the kernel reads the pending source page,
-    replays its accepted prefix exactly as the fold does (kernels.py:1222-1324),
-    stores the result to the final page (and the boundary snapshot), and
-    verifies this step's window from the folded state, so every page is read
-    once per step. Rows without a pending commit verify from
-    ``state_indices`` as ``gdn_recoverssm_verify`` does.
+    For each row that continues a pending commit (``pending.rows``) and whose
+    state index is that commit's final page, the kernel reads the pending
+    source page, replays its accepted prefix exactly as the fold does
+    (kernels.py:1222-1324), stores the result to the final page (and the
+    boundary snapshot), and verifies this step's window from the folded state,
+    so every page is read once per step. Other rows verify from
+    ``state_indices`` as ``gdn_recoverssm_verify`` does. Pending commits no row
+    applies stay pending (see ``continue_pending`` and ``flush_deferred``).
+    With no token in the batch the launch still applies the pending commits.
     """
     rec = pending.records
     _require(isinstance(rec, ReplayRecordBuffers), "the deferred commit needs typed record buffers")
@@ -349,23 +390,33 @@ def gdn_recoverssm_verify_deferred(
         rec.correction.data_ptr() != replay_cache.correction.data_ptr(),
         "the pending commit's records must not be the records this verify writes",
     )
-    _require(checkpoint_state.dtype == torch.float32, "the deferred commit is built for FP32 state")
     batch = state_indices.shape[0]
-    arrays = (pending.rows, pending.source, pending.lengths, pending.final, pending.boundary, pending.boundary_len)
+    num_rows = int(pending.num_rows)
+    if num_rows <= 0:
+        # Nothing is pending: the ordinary verify.
+        return gdn_recoverssm_verify(g, beta, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
+                                     query_start_loc=query_start_loc, state_indices=state_indices,
+                                     spec_query_len=spec_query_len, scale=scale,
+                                     qk_already_normalized=qk_already_normalized, out=out, _collect=_collect)
+    plan = (pending.source, pending.lengths, pending.final, pending.boundary, pending.boundary_len)
     _require(
-        all(t_.dtype == torch.int32 and t_.ndim == 1 and t_.shape[0] >= batch and t_.stride(0) == 1 for t_ in arrays),
-        "pending plan arrays must be contiguous int32 covering every row",
+        all(t_.dtype == torch.int32 and t_.ndim == 1 and t_.stride(0) == 1 for t_ in (pending.rows,) + plan),
+        "pending arrays must be contiguous one-dimensional int32",
     )
+    _require(pending.rows.shape[0] >= batch, "the pending row map does not cover the batch")
+    _require(all(t_.shape[0] >= num_rows for t_ in plan), "pending plan arrays do not cover their rows")
+    _require(num_rows <= rec.correction.shape[0], "the pending plan has more rows than its records")
     _require(
         rec.correction.shape[1:] == replay_cache.correction.shape[1:] and rec.key.shape[1:] == replay_cache.key.shape[1:],
         "pending records do not match this layer's record geometry",
     )
+    arrays = (pending.rows,) + plan
     pc = N.PendingCommit(
         rows=arrays[0].data_ptr(), source=arrays[1].data_ptr(), lengths=arrays[2].data_ptr(),
         final_indices=arrays[3].data_ptr(), boundary_indices=arrays[4].data_ptr(),
         boundary_lengths=arrays[5].data_ptr(), correction=rec.correction.data_ptr(), key=rec.key.data_ptr(),
         decay=rec.decay.data_ptr(), record_rows=rec.correction.shape[0],
-        key_dtype=N.dtype_code(rec.key.dtype), key_per_value_head=0,
+        key_dtype=N.dtype_code(rec.key.dtype), key_per_value_head=0, num_rows=num_rows,
     )
     for i in range(3):
         pc.corr_strides[i] = rec.correction.stride(i)
@@ -1092,6 +1143,7 @@ class GDNRecoverSSMCommitContext:
                     mamba_block_size=mamba_block_size, commit_conv=commit_conv, _collect=specs,
                     _fold_source=self.plan_source)
         self._deferred_fold = next(sp for sp in specs if sp.name == "fold")
+        self._deferred_rows = int(state_indices.shape[0])
         now = [sp for sp in specs if sp.name != "fold"]
         if _collect is not None:
             _collect.extend(now)
@@ -1100,14 +1152,37 @@ class GDNRecoverSSMCommitContext:
                 sp.launch()
         return tuple(
             PendingCommit(self.pending_rows, self.plan_source, self.commit_lens, self.final_state_indices,
-                          self.boundary_state_indices, self.boundary_recovery_lens, rec)
+                          self.boundary_state_indices, self.boundary_recovery_lens, rec,
+                          num_rows=self._deferred_rows)
             for rec in self.records
         )
 
-    def flush_deferred(self, _collect: list | None = None) -> None:
-        """Apply the last ``commit_deferred`` plan with the ordinary fold."""
+    def flush_deferred(self, rows: Sequence[int] | torch.Tensor | None = None, _collect: list | None = None) -> None:
+        """Apply the last ``commit_deferred`` plan with the ordinary fold.
+
+        ``rows=None`` folds every planned row (a step that runs no verify
+        after it, e.g. the end of a batch); a list of pending rows folds only
+        those (rows whose request left the batch, see ``continue_pending``),
+        leaving the rest to the next verify. A row must be folded once: by a
+        flush or by the verify that continues it, never both.
+        """
         spec = getattr(self, "_deferred_fold", None)
         _require(spec is not None, "no deferred commit to flush")
+        if rows is not None:
+            pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
+            _require(
+                bool(((pick >= 0) & (pick < self._deferred_rows)).all()),
+                "flushed rows must be rows of the pending plan",
+            )
+            if pick.numel() == 0:
+                return
+            # The same fold over a length array that keeps only the picked rows.
+            lengths = torch.zeros_like(self.commit_lens)
+            idx = pick.to(lengths.device)
+            lengths[idx] = self.commit_lens[idx]
+            args = list(spec.args)
+            args[14] = lengths.data_ptr()  # fold arguments: ..., source, lengths, finals, ...
+            spec = _LaunchSpec(spec.name, spec.fn, tuple(args), spec.device, keepalive=spec.keepalive + (lengths,))
         if _collect is not None:
             _collect.append(spec)
         else:

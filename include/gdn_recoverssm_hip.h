@@ -129,12 +129,14 @@ int gdn_recoverssm_verify_gated(const void *q, const void *k, const void *v, con
                                 const gdn_gating_ext *gating, void *stream);
 
 /* The previous step's commit of one layer, left for the next verify to apply.
- * Plan arrays (DEVICE, int32, indexed by the CURRENT step's row): `rows` gives
- * the record row of the pending commit (-1: none), the rest are the plan
- * outputs of that commit (source, accepted length, final, boundary, boundary
- * length; see gdn_recoverssm_plan). The records are the previous step's typed
- * SoA planes (or packed FP32 rows, key_per_value_head = 1); they must not be
- * the buffers the current verify writes. Strides in elements. */
+ * DEVICE arrays, int32: `rows` [current rows] gives for each row of the
+ * current batch the PENDING row it continues (the row of the previous step's
+ * plan and records; -1 or any value outside [0, num_rows) for none). The plan
+ * arrays of that commit (source, accepted length, final, boundary, boundary
+ * length; see gdn_recoverssm_plan) are indexed by pending row and cover
+ * `num_rows` (>= 1) rows. The records are the previous step's typed SoA planes
+ * (or packed FP32 rows, key_per_value_head = 1); they must not be the buffers
+ * the current verify writes. Strides in elements. */
 typedef struct gdn_pending_commit {
   const int32_t *rows;
   const int32_t *source;
@@ -151,17 +153,23 @@ typedef struct gdn_pending_commit {
   int64_t decay_strides[3];
   int32_t key_dtype;
   int32_t key_per_value_head;
+  int64_t num_rows;           /* rows of the pending plan (the previous step's batch) */
 } gdn_pending_commit;
 
-/* Verify with the previous step's commit folded in (FP32 state only; no
- * counterpart entry in the reference, whose design notes propose it). For
- * every row with a pending commit, the wave reads the pending source page,
- * replays the accepted prefix exactly as gdn_recoverssm_fold does, stores the
- * result to the final page (and the boundary snapshot), and verifies the
- * current window from the folded state; state_indices is not read for such a
- * row (it is expected to name the pending final page). Rows without a pending
- * commit verify from state_indices as gdn_recoverssm_verify does. A pending
- * commit must appear under some current row, and rows must not share pages. */
+/* Verify with the previous step's commit folded in (no counterpart entry in
+ * the reference, whose design notes propose it). A current row applies the
+ * pending commit of the row `rows` names when that commit is valid (accepted
+ * length 1..Q, source and final pages in range) and the row's own state index
+ * equals the commit's final page: the wave then reads the pending source page,
+ * replays the accepted prefix exactly as gdn_recoverssm_fold does (FP32
+ * arithmetic, stores rounded to the state type), stores the result to the
+ * final page (and the boundary snapshot), and verifies the current window
+ * from the folded state as stored. Every other row verifies from its own
+ * state index as gdn_recoverssm_verify does, and a pending commit no current
+ * row applies stays pending: flush it with gdn_recoverssm_fold before its
+ * pages are reused. Rows must not share pages. With no token in the batch the
+ * launch still applies the pending commits (q, k, v, g, beta and out may then
+ * be NULL). */
 int gdn_recoverssm_verify_deferred(const void *q, const void *k, const void *v, const void *g, const void *beta,
                                    const void *state, void *correction, void *key, void *decay, void *out,
                                    const void *qsl, const void *indices, const int64_t *config,

@@ -112,6 +112,7 @@ int main(void) {
   F(gdn_plan_launch, groups) F(gdn_plan_launch, col_plan) F(gdn_plan_launch, idx_mapping_dtype)
   F(gdn_plan_launch, flags) F(gdn_plan_launch, persistent_len) F(gdn_plan_launch, spec_query_len)
   F(gdn_pending_commit, record_rows) F(gdn_pending_commit, decay_strides) F(gdn_pending_commit, key_per_value_head)
+  F(gdn_pending_commit, num_rows)
   F(gdn_gating_ext, softplus_beta) F(gdn_gating_ext, softplus_threshold)
   F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
   F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride)

@@ -1,21 +1,40 @@
 """The deferred commit: the fold of step k applied inside step k+1's verify
-(``gdn_recoverssm_verify_deferred``) must give bit-for-bit what the ordinary
-flow gives (verify, then commit: plan + conv + fold), step after step: the
-same outputs and records every step and the same pages once the last pending
-fold is flushed. The ordinary flow itself is checked against the oracle in
-test_gpu_verify / test_gpu_commit / test_gpu_loop.
+(``gdn_recoverssm_verify_deferred``), checked two ways.
+
+* Against the CPU oracle, step by step: after each deferred verify every page
+  equals the oracle's fold of the previous step (pages outside that commit
+  bit-identical), this step's outputs and records equal ``oracle_verify`` from
+  those pages, and the plan equals ``oracle_plan_single`` bit for bit; after
+  the final flush the pages equal the oracle's last fold.
+* Against the ordinary flow (verify, then commit: plan + fold + conv), bit for
+  bit: outputs, records, plans, pages and conv states.
+
+Batch changes between steps go through ``continue_pending`` (rows keyed by
+request) and ``flush_deferred(rows=...)`` (the commits of requests that left),
+and are checked against the oracle as well: a request that leaves with an
+align-mode commit that crosses a block boundary, a new request taking a row,
+a reordered batch, a batch that grows past the pending plan's rows, and a
+step without a single token.
+
+Bar: plan and page indexing bit-exact; FP32 pages within max-abs 1e-5
+relative to the pages' max-abs (16-bit pages within 8e-3, one rounding);
+outputs within 1e-2 norm-wise; corrections within 1e-5 norm-wise; keys
+bit-exact; decays within 2 FP32 ulp.
 """
 
 import pytest
 import torch
 
+import gdn_oracle as O
 from gdn_recoverssm_ascend import workloads as W
 from gdn_recoverssm_ascend.kernels import (
     GDNRecoverSSMCommitContext,
     ReplayRecordBuffers,
+    continue_pending,
     gdn_recoverssm_verify,
     gdn_recoverssm_verify_deferred,
 )
+from gpu_helpers import CORR_TOL, OUT_TOL, assert_norm_close, assert_state_close
 
 pytestmark = pytest.mark.gpu
 
@@ -23,6 +42,176 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def dev(gpu_device):
     return gpu_device
+
+
+def _check_pages(got, want, touched, what):
+    """Pages outside `touched` bit-identical, the rest within the state bar."""
+    got = got.cpu()
+    untouched = [p for p in range(got.shape[0]) if p not in touched]
+    assert torch.equal(got[untouched], want[untouched]), f"{what}: pages outside the commit changed"
+    if want.dtype == torch.float32:
+        assert_state_close(got, want, what)
+    else:
+        err = O.max_abs_rel(got, want)
+        assert err <= 8e-3, f"{what}: max-abs error / max-abs = {err:.3g} > 8e-3"
+
+
+def _check_verify(out, rec, r, what):
+    """GPU outputs and records of one layer against an oracle VerifyResult."""
+    got = out.cpu()[0]
+    wm = r.out_written
+    if bool(wm.any()):
+        assert_norm_close(got[wm].double(), r.out[wm], OUT_TOL, f"{what} out")
+    rw = r.record_written  # [R, Q]
+    if not bool(rw.any()):
+        return
+    R = rw.shape[0]
+    corr, key, decay = rec.correction[:R].cpu(), rec.key[:R].cpu(), rec.decay[:R].cpu()
+    m_c = rw[:, None, :, None].expand_as(corr)
+    assert_norm_close(corr[m_c].double(), r.correction[m_c], CORR_TOL, f"{what} correction")
+    m_d = rw[:, None, :].expand_as(decay)
+    torch.testing.assert_close(decay[m_d].double(), r.decay[m_d], rtol=3e-7, atol=0)
+    m_k = rw[:, None, :, None].expand_as(key)
+    assert torch.equal(key[m_k].float(), r.key[m_k].float()), f"{what}: keys must keep the input bits"
+
+
+def _touched(plan, rows, num_pages):
+    n, fin, bnd, blen = (plan[k][:rows] for k in ("commit_lens", "final", "boundary", "boundary_len"))
+    pages = set()
+    for i in range(rows):
+        if int(n[i]) > 0:
+            pages.add(int(fin[i]))
+            if 0 < int(bnd[i]) < num_pages and int(bnd[i]) != int(fin[i]) and 0 < int(blen[i]) <= int(n[i]):
+                pages.add(int(bnd[i]))
+    return pages
+
+
+def _oracle_fold(pages, results, plan, rows, num_pages, lengths=None):
+    return O.oracle_fold(pages, [r.correction for r in results], [r.key for r in results],
+                         [r.decay for r in results], source=plan["source"],
+                         lengths=plan["commit_lens"] if lengths is None else lengths, final=plan["final"],
+                         boundary=plan["boundary"], boundary_len=plan["boundary_len"], rows=rows,
+                         num_blocks=num_pages, record_rows=rows, out_dtype=pages[0].dtype)
+
+
+def _step_inputs(w, layer, T):
+    i = w.inputs[layer]
+    return i.g[:T], i.beta[:T], i.q[:, :T], i.k[:, :T], i.v[:, :T]
+
+
+def _run_against_oracle(w, dev, acc_steps, qsl_steps):
+    """The deferred flow over len(acc_steps) carried steps, each checked
+    against the oracle as described in the module docstring."""
+    s = w.spec
+    L, B, Q, H, HV, K, V = s.layers, s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+    wd = w.to(dev)
+    ckpts = [c.clone() for c in wd.checkpoints]
+    convs = [c.clone() for c in wd.conv_states]
+    recs = [[ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=wd.inputs[0].k.dtype)
+             for _ in range(L)] for _ in range(2)]
+    ctxs = [GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs[i], spec_query_len=Q, max_num_reqs=B)
+            for i in range(2)]
+    state_idx = wd.meta.state_indices.clone()
+    computed = wd.meta.num_computed.clone()
+    src_cpu = w.meta.state_indices.clone()
+    c_cpu = w.meta.num_computed.clone()
+    want = [c.clone() for c in w.checkpoints]
+    touched = set()
+    pending = None
+    commits = crossings = 0
+    for step, (acc, qsl) in enumerate(zip(acc_steps, qsl_steps)):
+        i = step % 2
+        T = int(qsl[-1])
+        qd = qsl.to(dev)
+        outs = []
+        for layer in range(L):
+            kw = dict(checkpoint_state=ckpts[layer], replay_cache=recs[i][layer], query_start_loc=qd,
+                      state_indices=state_idx, spec_query_len=Q)
+            args = _step_inputs(wd, layer, T)
+            if pending is None:
+                outs.append(gdn_recoverssm_verify(*args, **kw))
+            else:
+                outs.append(gdn_recoverssm_verify_deferred(*args, pending=pending[layer], **kw))
+        torch.cuda.synchronize()
+        cur = []
+        for layer in range(L):
+            _check_pages(ckpts[layer], want[layer], touched, f"step {step} layer {layer}: pages after the verify")
+            cur.append(ckpts[layer].cpu())
+        results = []
+        for layer in range(L):
+            ci = w.inputs[layer]
+            r = O.oracle_verify(ci.q[:, :T], ci.k[:, :T], ci.v[:, :T], ci.g[:T], ci.beta[:T], cur[layer], qsl, src_cpu, Q)
+            _check_verify(outs[layer], recs[i][layer], r, f"step {step} layer {layer}")
+            results.append(r)
+        pending = ctxs[i].commit_deferred(acc.to(dev), state_idx, qd, block_table=wd.meta.block_table,
+                                          num_computed_tokens=computed, mamba_block_size=s.block_size)
+        plan = O.oracle_plan_single(acc, src_cpu, qsl, spec_query_len=Q, num_blocks=w.num_pages,
+                                    block_table=w.meta.block_table, num_computed=c_cpu, block_size=s.block_size)
+        ctx = ctxs[i]
+        for name, t in (("commit_lens", ctx.commit_lens), ("final", ctx.final_state_indices),
+                        ("boundary", ctx.boundary_state_indices), ("boundary_len", ctx.boundary_recovery_lens)):
+            assert t[:B].cpu().tolist() == plan[name].tolist(), f"step {step}: plan {name} differs"
+        plan["source"] = src_cpu
+        want = _oracle_fold(cur, results, plan, B, w.num_pages)
+        touched = _touched(plan, B, w.num_pages)
+        commits += int((plan["commit_lens"] > 0).sum())
+        crossings += len(touched) - int((plan["commit_lens"] > 0).sum())
+        n = plan["commit_lens"]
+        src_cpu = torch.where(n > 0, plan["final"], src_cpu).to(torch.int32)
+        c_cpu = (c_cpu + n).to(c_cpu.dtype)
+        lens = ctx.commit_lens[:B]
+        state_idx.copy_(torch.where(lens > 0, ctx.final_state_indices[:B], state_idx))
+        computed.add_(lens.to(computed.dtype))
+    ctxs[(len(acc_steps) - 1) % 2].flush_deferred()
+    torch.cuda.synchronize()
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the flush")
+    assert commits > 0 and crossings > 0, "the steps committed nothing or crossed no block boundary"
+
+
+@pytest.mark.parametrize("seed,empty_row,state_dtype", [
+    (5, None, torch.float32),
+    (9, 3, torch.float32),
+    (13, None, torch.bfloat16),
+    (17, 2, torch.float16),
+])
+def test_deferred_commit_against_oracle(dev, seed, empty_row, state_dtype):
+    """Four carried steps, align mode with boundary crossings and a padded
+    row; with `empty_row`, step 2 gives that row no token while it carries a
+    pending commit (the verify must fold it anyway)."""
+    steps = 4
+    w = W.make_workload("decode_loop_l48", layers=2, rows=10, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=steps, max_position=512, block_size=8, padded_rows=1, seed=seed,
+                        state_dtype=state_dtype)
+    s = w.spec
+    print(f"deferred vs oracle: seed={seed} empty_row={empty_row} state={state_dtype}", flush=True)
+    gen = torch.Generator().manual_seed(seed + 1)
+    acc_steps = [W.sample_accepted(s, s.rows, gen) for _ in range(steps)]
+    qsl_steps = [w.meta.query_start_loc.clone() for _ in range(steps)]
+    if empty_row is not None:
+        lens = torch.full((s.rows,), s.window, dtype=torch.int32)
+        lens[empty_row] = 0
+        q2 = torch.zeros(s.rows + 1, dtype=torch.int32)
+        q2[1:] = torch.cumsum(lens, 0)
+        qsl_steps[2] = q2
+    _run_against_oracle(w, dev, acc_steps, qsl_steps)
+
+
+def test_deferred_step_without_tokens(dev):
+    """A step whose batch has no token at all while every row carries a
+    pending commit: the launch still applies the commits (g, beta, q, k, v
+    are empty tensors, so their pointers are null) and the pages equal the
+    oracle's fold; the next step verifies from them."""
+    steps = 3
+    w = W.make_workload("decode_loop_l48", layers=1, rows=8, key_heads=2, value_heads=4, key_dim=128, value_dim=64,
+                        steps=steps, max_position=256, block_size=8, padded_rows=1, seed=31)
+    s = w.spec
+    gen = torch.Generator().manual_seed(32)
+    acc_steps = [torch.full((s.rows,), s.window, dtype=torch.int32)] + [W.sample_accepted(s, s.rows, gen)
+                                                                        for _ in range(steps - 1)]
+    qsl_steps = [w.meta.query_start_loc.clone(), torch.zeros(s.rows + 1, dtype=torch.int32),
+                 w.meta.query_start_loc.clone()]
+    _run_against_oracle(w, dev, acc_steps, qsl_steps)
 
 
 def _flow(w, dev, acc_steps, qsl_steps, *, deferred):
@@ -44,9 +233,8 @@ def _flow(w, dev, acc_steps, qsl_steps, *, deferred):
         qsl = qsl.to(dev)
         outs = []
         for layer in range(L):
-            inp = wd.inputs[layer]
             T = int(qsl[-1])
-            args = (inp.g[:T], inp.beta[:T], inp.q[:, :T], inp.k[:, :T], inp.v[:, :T])
+            args = _step_inputs(wd, layer, T)
             kw = dict(checkpoint_state=ckpts[layer], replay_cache=recs[i][layer], query_start_loc=qsl,
                       state_indices=state_idx, spec_query_len=Q)
             if deferred and pending is not None:
@@ -79,6 +267,20 @@ def _flow(w, dev, acc_steps, qsl_steps, *, deferred):
     return history, ckpts, convs
 
 
+def _assert_flows_equal(ref, got):
+    (ref_h, ref_pages, ref_convs), (got_h, got_pages, got_convs) = ref, got
+    for step, (a, b) in enumerate(zip(ref_h, got_h)):
+        for name in ("out", "corr", "key", "decay", "plan"):
+            for li, (x, y) in enumerate(zip(a[name], b[name])):
+                assert torch.equal(x, y), f"step {step} {name} [{li}] differs"
+        assert torch.equal(a["state_idx"], b["state_idx"])
+    for li, (x, y) in enumerate(zip(ref_pages, got_pages)):
+        assert torch.equal(x, y), f"layer {li}: pages differ after the flush"
+    for li, (x, y) in enumerate(zip(ref_convs, got_convs)):
+        assert torch.equal(x, y), f"layer {li}: conv states differ"
+    assert sum(int((h["plan"][0] > 0).sum()) for h in ref_h) > 0
+
+
 @pytest.mark.parametrize("seed,empty_row", [(5, None), (9, 3)])
 def test_deferred_commit_equals_ordinary_flow(dev, seed, empty_row):
     steps = 4
@@ -89,108 +291,190 @@ def test_deferred_commit_equals_ordinary_flow(dev, seed, empty_row):
     acc_steps = [W.sample_accepted(s, s.rows, gen) for _ in range(steps)]
     qsl_steps = [w.meta.query_start_loc.clone() for _ in range(steps)]
     if empty_row is not None:
-        # Step 2 has no token for one row that still carries a pending commit:
-        # the deferred verify must fold it anyway.
         lens = torch.full((s.rows,), s.window, dtype=torch.int32)
         lens[empty_row] = 0
         q2 = torch.zeros(s.rows + 1, dtype=torch.int32)
         q2[1:] = torch.cumsum(lens, 0)
         qsl_steps[2] = q2
-    ref, ref_pages, ref_convs = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
-    got, got_pages, got_convs = _flow(w, dev, acc_steps, qsl_steps, deferred=True)
-    for step, (a, b) in enumerate(zip(ref, got)):
-        for name in ("out", "corr", "key", "decay", "plan"):
-            for li, (x, y) in enumerate(zip(a[name], b[name])):
-                assert torch.equal(x, y), f"step {step} {name} [{li}] differs"
-        assert torch.equal(a["state_idx"], b["state_idx"])
-    for li, (x, y) in enumerate(zip(ref_pages, got_pages)):
-        assert torch.equal(x, y), f"layer {li}: pages differ after the flush"
-    for li, (x, y) in enumerate(zip(ref_convs, got_convs)):
-        assert torch.equal(x, y), f"layer {li}: conv states differ"
-    # the comparison is not vacuous: commits happened and crossed boundaries
-    assert sum(int((h["plan"][0] > 0).sum()) for h in ref) > 0
-    assert sum(int((h["plan"][2] > 0).sum()) for h in ref) > 0
+    ref = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
+    got = _flow(w, dev, acc_steps, qsl_steps, deferred=True)
+    _assert_flows_equal(ref, got)
+    assert sum(int((h["plan"][2] > 0).sum()) for h in ref[0]) > 0
 
 
-@pytest.mark.parametrize("K,V,Q,H,HV,act", [
-    (64, 100, 3, 1, 4, torch.bfloat16),
-    (256, 64, 8, 2, 2, torch.bfloat16),
-    (32, 192, 1, 2, 8, torch.float16),
-    (136, 48, 5, 3, 6, torch.float32),
-    (96, 16, 6, 1, 1, torch.bfloat16),
+@pytest.mark.parametrize("K,V,Q,H,HV,act,state", [
+    (64, 100, 3, 1, 4, torch.bfloat16, torch.float32),
+    (256, 64, 8, 2, 2, torch.bfloat16, torch.float32),
+    (32, 192, 1, 2, 8, torch.float16, torch.float32),
+    (136, 48, 5, 3, 6, torch.float32, torch.float32),
+    (96, 16, 6, 1, 1, torch.bfloat16, torch.float32),
+    (128, 128, 4, 2, 4, torch.bfloat16, torch.bfloat16),
+    (64, 72, 3, 1, 2, torch.float16, torch.float16),
+    (256, 40, 8, 2, 4, torch.float32, torch.bfloat16),
 ])
-def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act):
+def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act, state):
     """The same equality over head dims off the 128 x 128 tile (partial
-    64-row half tiles, K padded to whole chunks), windows 1-8, GQA ratios 1-4
-    and every activation dtype."""
+    64-row half tiles, K padded to whole chunks), windows 1-8, GQA ratios 1-4,
+    every activation dtype and every state dtype."""
     steps = 3
     w = W.make_workload("decode_loop_l48", layers=2, rows=6, key_heads=H, value_heads=HV, key_dim=K, value_dim=V,
-                        window=Q, act_dtype=act, steps=steps, max_position=256, block_size=8, padded_rows=1,
-                        seed=K + V + Q)
+                        window=Q, act_dtype=act, state_dtype=state, steps=steps, max_position=256, block_size=8,
+                        padded_rows=1, seed=K + V + Q)
     s = w.spec
-    print(f"deferred shapes: K={K} V={V} Q={Q} H={H} HV={HV} act={act}", flush=True)
+    print(f"deferred shapes: K={K} V={V} Q={Q} H={H} HV={HV} act={act} state={state}", flush=True)
     gen = torch.Generator().manual_seed(K * V + Q)
     acc_steps = [W.sample_accepted(s, s.rows, gen) for _ in range(steps)]
     qsl_steps = [w.meta.query_start_loc.clone() for _ in range(steps)]
-    ref, ref_pages, ref_convs = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
-    got, got_pages, got_convs = _flow(w, dev, acc_steps, qsl_steps, deferred=True)
-    for step, (a, b) in enumerate(zip(ref, got)):
-        for name in ("out", "corr", "key", "decay", "plan"):
-            for li, (x, y) in enumerate(zip(a[name], b[name])):
-                assert torch.equal(x, y), f"step {step} {name} [{li}] differs"
-    for li, (x, y) in enumerate(zip(ref_pages, got_pages)):
-        assert torch.equal(x, y), f"layer {li}: pages differ after the flush"
-    for li, (x, y) in enumerate(zip(ref_convs, got_convs)):
-        assert torch.equal(x, y), f"layer {li}: conv states differ"
-    assert sum(int((h["plan"][0] > 0).sum()) for h in ref) > 0
+    _assert_flows_equal(_flow(w, dev, acc_steps, qsl_steps, deferred=False),
+                        _flow(w, dev, acc_steps, qsl_steps, deferred=True))
 
 
-def test_deferred_commit_with_reordered_rows(dev):
-    """The next step's batch lists the rows in another order: the pending
-    commit's arrays are indexed by the next step's row and ``rows`` points at
-    the record row the pending step wrote (row b of the new batch is old row
-    perm[b]). Outputs, records and folded pages equal the ordinary flow's."""
-    from gdn_recoverssm_ascend.kernels import PendingCommit
-
-    w = W.make_workload("decode_loop_l48", layers=1, rows=8, key_heads=2, value_heads=4, steps=2, max_position=256,
-                        block_size=8, padded_rows=1, seed=21)
+def _first_step(w, dev, acc):
+    """Step 0 on the GPU: ordinary verify, then commit_deferred. Returns the
+    device state, the pending commits, the oracle results and plan."""
     s = w.spec
-    B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
-    gen = torch.Generator().manual_seed(22)
-    acc0 = W.sample_accepted(s, B, gen)
-    perm = torch.randperm(B, generator=gen)
+    L, B, Q, H, HV, K, V = s.layers, s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
     wd = w.to(dev)
-    inp, m = wd.inputs[0], wd.meta
-    kw = dict(block_table=m.block_table, num_computed_tokens=m.num_computed, mamba_block_size=s.block_size)
-    results = []
-    for deferred in (False, True):
-        ckpt, conv = wd.checkpoints[0].clone(), wd.conv_states[0].clone()
-        recs = [ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype) for _ in range(2)]
-        ctx = GDNRecoverSSMCommitContext.from_tensors([conv], [ckpt], [recs[0]], spec_query_len=Q, max_num_reqs=B)
-        idx0 = m.state_indices.clone()
-        args = (inp.g, inp.beta, inp.q, inp.k, inp.v)
-        gdn_recoverssm_verify(*args, checkpoint_state=ckpt, replay_cache=recs[0], query_start_loc=m.query_start_loc,
-                              state_indices=idx0, spec_query_len=Q)
-        if deferred:
-            pend = ctx.commit_deferred(acc0.to(dev), idx0, m.query_start_loc, **kw)[0]
-        else:
-            ctx.commit(acc0.to(dev), idx0, m.query_start_loc, **kw)
-        lens = ctx.commit_lens[:B]
-        idx1 = torch.where(lens > 0, ctx.final_state_indices[:B], idx0)[perm.to(dev)].contiguous()
-        kw1 = dict(checkpoint_state=ckpt, replay_cache=recs[1], query_start_loc=m.query_start_loc,
-                   state_indices=idx1, spec_query_len=Q)
-        if deferred:
-            p = perm.to(dev)
-            moved = PendingCommit(pend.rows[p].contiguous(), pend.source[p].contiguous(), pend.lengths[p].contiguous(),
-                                  pend.final[p].contiguous(), pend.boundary[p].contiguous(),
-                                  pend.boundary_len[p].contiguous(), pend.records)
-            out = gdn_recoverssm_verify_deferred(*args, pending=moved, **kw1)
-        else:
-            out = gdn_recoverssm_verify(*args, **kw1)
-        torch.cuda.synchronize()
-        results.append([out.clone(), recs[1].correction.clone(), recs[1].key.clone(), recs[1].decay.clone(),
-                        ckpt.clone()])
-        if not deferred:
-            assert int((lens > 0).sum()) > 0 and not torch.equal(perm, torch.arange(B))
-    for name, a, b in zip(("out", "correction", "key", "decay", "pages"), *results):
-        assert torch.equal(a, b), f"{name} differs"
+    ckpts = [c.clone() for c in wd.checkpoints]
+    convs = [c.clone() for c in wd.conv_states]
+    recs = [[ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=wd.inputs[0].k.dtype)
+             for _ in range(L)] for _ in range(2)]
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs[0], spec_query_len=Q, max_num_reqs=2 * B)
+    m = wd.meta
+    for layer in range(L):
+        gdn_recoverssm_verify(*_step_inputs(wd, layer, w.tokens), checkpoint_state=ckpts[layer],
+                              replay_cache=recs[0][layer], query_start_loc=m.query_start_loc,
+                              state_indices=m.state_indices, spec_query_len=Q)
+    pending = ctx.commit_deferred(acc.to(dev), m.state_indices, m.query_start_loc, block_table=m.block_table,
+                                  num_computed_tokens=m.num_computed, mamba_block_size=s.block_size)
+    cm = w.meta
+    results = [O.oracle_verify(i.q, i.k, i.v, i.g, i.beta, c, cm.query_start_loc, cm.state_indices, Q)
+               for i, c in zip(w.inputs, w.checkpoints)]
+    plan = O.oracle_plan_single(acc, cm.state_indices, cm.query_start_loc, spec_query_len=Q, num_blocks=w.num_pages,
+                                block_table=cm.block_table, num_computed=cm.num_computed, block_size=s.block_size)
+    plan["source"] = cm.state_indices.clone()
+    torch.cuda.synchronize()
+    for name, t in (("commit_lens", ctx.commit_lens), ("final", ctx.final_state_indices),
+                    ("boundary", ctx.boundary_state_indices)):
+        assert t[:B].cpu().tolist() == plan[name].tolist(), f"step 0: plan {name} differs"
+    return dict(ckpts=ckpts, recs=recs, ctx=ctx, pending=pending, results=results, plan=plan)
+
+
+def test_batch_change_with_flush(dev):
+    """Step 1 keeps most requests in a shuffled order, drops two (one of them
+    with an align-mode commit that writes a boundary snapshot) and admits a
+    new request on a page of its own. The row map comes from
+    ``continue_pending``; the verify applies the continued requests' commits
+    and ``flush_deferred(rows=left)`` the departed ones'. Every page then
+    equals the oracle's fold of step 0, the departed rows' final and boundary
+    pages included, and step 1's outputs equal the oracle's verify from those
+    pages (the new request's from its own unfolded page)."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=41)
+    s = w.spec
+    L, B, Q = s.layers, s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[::3] = 2
+    st = _first_step(w, dev, acc)
+    plan = st["plan"]
+    n, fin, bnd = plan["commit_lens"], plan["final"], plan["boundary"]
+    pad = int(w.extras["padded_rows"][0])
+    crossing = [r for r in range(B) if int(n[r]) > 0 and int(bnd[r]) > 0 and int(bnd[r]) != int(fin[r])]
+    plain = [r for r in range(B) if int(n[r]) > 0 and r not in crossing]
+    assert crossing and plain, "the seed must give a crossing and a plain commit"
+    leaving = [crossing[0], plain[0]]
+    gen = torch.Generator().manual_seed(42)
+    stay = [r for r in range(B) if r not in leaving and r != pad]
+    stay = [stay[i] for i in torch.randperm(len(stay), generator=gen).tolist()]
+    new_request = 1000
+    next_requests = stay[:3] + [new_request] + stay[3:]
+    B1 = len(next_requests)
+    # Step-1 metadata: continued requests from their committed page and
+    # position, the new request from the padded row's own (never written) page.
+    src_col = w.extras["source_col"]
+    table = w.meta.block_table
+    new_page = int(table[pad, src_col[pad]])
+    idx1 = torch.tensor([new_page if r == new_request else (int(fin[r]) if int(n[r]) > 0 else
+                                                            int(w.meta.state_indices[r])) for r in next_requests],
+                        dtype=torch.int32)
+    qsl1 = torch.arange(B1 + 1, dtype=torch.int32) * Q
+    inputs1 = [W.make_layer_inputs(s, B1 * Q, gen) for _ in range(L)]
+    pending1, left = continue_pending(st["pending"], list(range(B)), next_requests)
+    assert left == sorted(leaving + [pad])
+    assert pending1[0].rows.cpu().tolist() == [-1 if r == new_request else r for r in next_requests]
+
+    ckpts, recs, ctx = st["ckpts"], st["recs"], st["ctx"]
+    qd, idx_d = qsl1.to(dev), idx1.to(dev)
+    outs = []
+    for layer in range(L):
+        i = inputs1[layer]
+        outs.append(gdn_recoverssm_verify_deferred(
+            i.g.to(dev), i.beta.to(dev), i.q.to(dev), i.k.to(dev), i.v.to(dev), checkpoint_state=ckpts[layer],
+            replay_cache=recs[1][layer], pending=pending1[layer], query_start_loc=qd, state_indices=idx_d,
+            spec_query_len=Q))
+    torch.cuda.synchronize()
+    # The departed requests' final pages are still unwritten: no verify applied them.
+    before = [c.cpu() for c in w.checkpoints]
+    for layer in range(L):
+        for r in leaving:
+            assert torch.equal(ckpts[layer][int(fin[r])].cpu(), before[layer][int(fin[r])]), "a departed fold ran"
+    ctx.flush_deferred(rows=left)
+    torch.cuda.synchronize()
+    want = _oracle_fold(before, st["results"], plan, B, w.num_pages)
+    touched = _touched(plan, B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after verify + flush")
+        for r in leaving:  # named explicitly: the departed rows' final (and boundary) pages
+            pages = [int(fin[r])] + ([int(bnd[r])] if r in crossing else [])
+            for p in pages:
+                assert_state_close(ckpts[layer][p].cpu(), want[layer][p], f"layer {layer}: departed row {r} page {p}")
+    for layer in range(L):
+        i = inputs1[layer]
+        r1 = O.oracle_verify(i.q, i.k, i.v, i.g, i.beta, want[layer], qsl1, idx1, Q)
+        _check_verify(outs[layer], recs[1][layer], r1, f"step 1 layer {layer}")
+
+
+def test_rows_past_the_pending_plan_do_not_apply(dev):
+    """The pending plan covers `num_rows` rows, and plan entries past them
+    (here: the rest of a full plan, as an older, larger step leaves them)
+    look valid. Rows of a larger next batch at or past `num_rows`, whose state
+    index equals such an entry's final page, must verify from their own page
+    and fold nothing; rows below it apply their commits. A row whose state
+    index is not its pending commit's final page (a new request in a
+    continued row) also verifies from its own page."""
+    from dataclasses import replace
+
+    w = W.make_workload("decode_loop_l48", layers=1, rows=10, key_heads=2, value_heads=4, key_dim=128, value_dim=64,
+                        steps=2, max_position=512, block_size=8, padded_rows=0, seed=51)
+    s = w.spec
+    B, Q = s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    st = _first_step(w, dev, acc)
+    plan = st["plan"]
+    n, fin = plan["commit_lens"], plan["final"]
+    src = w.meta.state_indices
+    B0 = 6
+    short = tuple(replace(p, num_rows=B0) for p in st["pending"])
+    idx1 = torch.where(n > 0, fin, src).to(torch.int32)
+    # One row below B0 keeps its pending row but names its source page, which
+    # differs from its commit's final page.
+    moved = [r for r in range(B0) if int(n[r]) > 0 and int(fin[r]) != int(src[r])]
+    assert moved and all(int(n[r]) > 0 for r in range(B0, B)), "the seed must move a row to a new page"
+    taken = moved[0]
+    idx1[taken] = int(src[taken])
+    gen = torch.Generator().manual_seed(52)
+    inp = W.make_layer_inputs(s, B * Q, gen)
+    qsl = w.meta.query_start_loc
+    ckpts, recs = st["ckpts"], st["recs"]
+    out = gdn_recoverssm_verify_deferred(inp.g.to(dev), inp.beta.to(dev), inp.q.to(dev), inp.k.to(dev),
+                                         inp.v.to(dev), checkpoint_state=ckpts[0], replay_cache=recs[1][0],
+                                         pending=short[0], query_start_loc=qsl.to(dev), state_indices=idx1.to(dev),
+                                         spec_query_len=Q)
+    torch.cuda.synchronize()
+    applied = torch.tensor([1 if (r < B0 and r != taken) else 0 for r in range(B)], dtype=torch.int32)
+    want = _oracle_fold([w.checkpoints[0]], st["results"][:1], plan, B, w.num_pages,
+                        lengths=plan["commit_lens"] * applied)
+    pages = _touched({**plan, "commit_lens": plan["commit_lens"] * applied}, B, w.num_pages)
+    _check_pages(ckpts[0], want[0], pages, "pages after a verify with a short pending plan")
+    r1 = O.oracle_verify(inp.q, inp.k, inp.v, inp.g, inp.beta, want[0], qsl, idx1, Q)
+    _check_verify(out, recs[1][0], r1, "step 1")
