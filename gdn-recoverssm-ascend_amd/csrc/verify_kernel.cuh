@@ -72,6 +72,16 @@ struct VerifyArgs {
   int32_t p_key_f32, p_key_per_value_head, p_record_rows, p_num_rows;
 };
 
+#ifndef GDN_V_STORE_END
+#define GDN_V_STORE_END 0
+#endif
+#ifndef GDN_V_POL_OUT
+#define GDN_V_POL_OUT 0
+#endif
+#ifndef GDN_V_POL_REC
+#define GDN_V_POL_REC 0
+#endif
+
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
 constexpr int kTileRows = 128;     // eight MFMA row blocks of 16 rows
 // The deferred-commit kernels stream half tiles: a wave that also stores the
@@ -185,8 +195,27 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ int64_t ld_idx(const void *p, int64_t i, bool i64) {
-  return i64 ? static_cast<const int64_t *>(p)[i] : int64_t(static_cast<const int32_t *>(p)[i]);
+// Wave-uniform words gathered by one vector load: every lane reads the 32-bit
+// word at its own address and readlane hands lane i's word to the whole wave.
+// A wave's offsets, slot, gates and pending plan are read this way, a few
+// words per lane-indexed load and one wait each, instead of one load and one
+// wait per word: as separate loads the compiler issued each only after the
+// previous one returned, and three serial round trips under the load of the
+// other waves' state streams took a third of a wave's life before its first
+// state load could issue.
+// Through the global address space: a flat load would also count against the
+// LDS / scalar counter, and every LDS wait would then wait for it.
+__device__ __forceinline__ uint32_t lane_word(uintptr_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t *>(addr);
+}
+__device__ __forceinline__ uint32_t word_of(uint32_t w, int i) { return uint32_t(__builtin_amdgcn_readlane(int(w), i)); }
+// int32 or int64 element from its low and high words (for int32 the high
+// word is a second read of the low one).
+__device__ __forceinline__ int64_t index_of(uint32_t lo, uint32_t hi, bool i64) {
+  return i64 ? int64_t((uint64_t(hi) << 32) | lo) : int64_t(int32_t(lo));
+}
+__device__ __forceinline__ uintptr_t elem_addr(const void *p, int64_t i, bool i64) {
+  return reinterpret_cast<uintptr_t>(p) + uintptr_t(i) * (i64 ? 8u : 4u);
 }
 
 // DEFER: before verifying, apply the previous step's commit for this row (the
@@ -220,12 +249,87 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const int V = a.V, K = a.K;
   const int row0 = vt * TILE;
   const int Q = a.Q;
+  constexpr int AS = int(sizeof(A));
 
-  const int64_t bos = ld_idx(a.qsl, int64_t(b) * a.qsl_s, a.qsl_i64);
-  const int64_t eos = ld_idx(a.qsl, int64_t(b + 1) * a.qsl_s, a.qsl_i64);
+  // ---- 0. the wave's metadata: one lane-indexed load, one wait ----
+  // Lanes 0-5: low and high words of query_start_loc[b], query_start_loc[b+1]
+  // and state_indices[b]; DEFER: lane 6 the pending row of b.
+  int64_t bos, eos, slot;
+  int prow = 0;
+  {
+    const uintptr_t q0 = elem_addr(a.qsl, int64_t(b) * a.qsl_s, a.qsl_i64);
+    const uintptr_t q1 = elem_addr(a.qsl, int64_t(b + 1) * a.qsl_s, a.qsl_i64);
+    const uintptr_t s0 = elem_addr(a.indices, int64_t(b) * a.idx_s, a.idx_i64);
+    const uintptr_t hq = a.qsl_i64 ? 4 : 0, hs = a.idx_i64 ? 4 : 0;
+    uintptr_t addr = q0;
+    addr = lane == 1 ? q0 + hq : addr;
+    addr = lane == 2 ? q1 : addr;
+    addr = lane == 3 ? q1 + hq : addr;
+    addr = lane == 4 ? s0 : addr;
+    addr = lane == 5 ? s0 + hs : addr;
+    if constexpr (DEFER) addr = lane == 6 ? reinterpret_cast<uintptr_t>(a.p_rows) + uintptr_t(b) * 4u : addr;
+    const uint32_t w = lane_word(addr);
+    bos = index_of(word_of(w, 0), word_of(w, 1), a.qsl_i64);
+    eos = index_of(word_of(w, 2), word_of(w, 3), a.qsl_i64);
+    slot = index_of(word_of(w, 4), word_of(w, 5), a.idx_i64);
+    if constexpr (DEFER) prow = int(word_of(w, 6));
+  }
   const int64_t qlen = eos - bos;
-  const int64_t slot = ld_idx(a.indices, int64_t(b) * a.idx_s, a.idx_i64);
   const int64_t out_base = int64_t(hv) * V + row0;
+  // Token validity is uniform across the wave (kernels.py:612).
+  uint32_t valid_mask = 0;
+#pragma unroll
+  for (int t = 0; t < QM; ++t) {
+    const int64_t tok = bos + t;
+    if (t < Q && t < qlen && tok >= 0 && tok < a.tokens) valid_mask |= 1u << t;
+  }
+
+  // ---- 1. gates (and DEFER: the pending plan and decays): one load ----
+  // Lane t < QM reads the dword holding g of token t, lane QM + t that of
+  // beta (FP32, or the 16-bit value at its half); tokens outside the window
+  // read the first word of query_start_loc (always present; g and beta may be
+  // empty, hence null, when the launch has no token at all) and are
+  // discarded. DEFER: lanes 2QM .. 2QM+4 read the pending row's accepted
+  // length, source, final and boundary pages and boundary length, and lanes
+  // 2QM+5 .. 3QM+4 its decays; a row without a pending row reads row 0
+  // (num_rows >= 1) and discards it. The ordinary kernel waits for these
+  // words only after its state loads issue; the deferred one needs the
+  // pending source page first.
+  const int gsz = a.g_f32 ? 4 : AS, bsz = a.beta_f32 ? 4 : AS;
+  const uintptr_t any_word = reinterpret_cast<uintptr_t>(a.qsl);
+  int gsh[QM], bsh[QM];
+  uint32_t gw;
+  const bool prow_ok = DEFER && prow >= 0 && prow < a.p_num_rows && prow < a.p_record_rows;
+  const int pr = prow_ok ? prow : 0;
+  {
+    uintptr_t addr = any_word;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const bool tv = (valid_mask >> t) & 1u;
+      const uintptr_t ga =
+          tv ? reinterpret_cast<uintptr_t>(a.g) + uintptr_t(((bos + t) * a.g_ts + hv) * gsz) : any_word;
+      const uintptr_t ba =
+          tv ? reinterpret_cast<uintptr_t>(a.beta) + uintptr_t(((bos + t) * a.beta_ts + hv) * bsz) : any_word;
+      gsh[t] = int(ga & 2) * 8;
+      bsh[t] = int(ba & 2) * 8;
+      addr = lane == t ? ga : addr;
+      addr = lane == QM + t ? ba : addr;
+    }
+    if constexpr (DEFER) {
+      const int32_t *plan[5] = {a.p_len, a.p_src, a.p_final, a.p_bnd, a.p_blen};
+#pragma unroll
+      for (int i = 0; i < 5; ++i)
+        addr = lane == 2 * QM + i ? reinterpret_cast<uintptr_t>(plan[i] + pr) : addr;
+#pragma unroll
+      for (int t = 0; t < QM; ++t) {
+        const uintptr_t da = reinterpret_cast<uintptr_t>(a.p_decay) +
+                             uintptr_t((int64_t(pr) * a.p_decay_rs + int64_t(hv) * a.p_decay_hs +
+                                        int64_t(t) * a.p_decay_ts) * 4);
+        addr = lane == 2 * QM + 5 + t ? (t < Q ? da : any_word) : addr;
+      }
+    }
+    gw = lane_word(addr & ~uintptr_t(3));
+  }
 
   // Pending commit of the previous step (same validity rule as the fold,
   // kernels.py:1232-1242 / csrc/fold.h:192-205). The row continues pending
@@ -234,17 +338,14 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   // whose metadata names another page, verifies from its own page and leaves
   // the pending commit to a flush.
   bool pend = false, pstore_b = false;
-  int pn = 0, pblen = 0, prow = 0;
+  int pn = 0, pblen = 0;
   int64_t psrc = 0, pfin = 0, pbnd = 0;
   if constexpr (DEFER) {
-    prow = int(ld_idx(a.p_rows, b, false));
-    const bool prow_ok = prow >= 0 && prow < a.p_num_rows && prow < a.p_record_rows;
-    const int pr = prow_ok ? prow : 0;  // p_num_rows >= 1: entry 0 exists
-    pn = int(ld_idx(a.p_len, pr, false));
-    psrc = ld_idx(a.p_src, pr, false);
-    pfin = ld_idx(a.p_final, pr, false);
-    pbnd = ld_idx(a.p_bnd, pr, false);
-    pblen = int(ld_idx(a.p_blen, pr, false));
+    pn = int(word_of(gw, 2 * QM + 0));
+    psrc = int(word_of(gw, 2 * QM + 1));
+    pfin = int(word_of(gw, 2 * QM + 2));
+    pbnd = int(word_of(gw, 2 * QM + 3));
+    pblen = int(word_of(gw, 2 * QM + 4));
     pend = prow_ok && pn > 0 && pn <= Q && psrc > a.null_block && psrc < a.blocks && pfin > a.null_block &&
            pfin < a.blocks && pfin == slot;
     pstore_b = pend && pbnd > a.null_block && pbnd < a.blocks && pbnd != pfin && pblen > 0 && pblen <= pn;
@@ -263,13 +364,6 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     }
     return;  // a pending commit needs slot == its final page, never a null one
   }
-  // Token validity is uniform across the wave (kernels.py:612).
-  uint32_t valid_mask = 0;
-#pragma unroll
-  for (int t = 0; t < QM; ++t) {
-    const int64_t tok = bos + t;
-    if (t < Q && t < qlen && tok >= 0 && tok < a.tokens) valid_mask |= 1u << t;
-  }
   if (valid_mask == 0 && !pend) return;
   // A pending commit on a row with nothing to verify still has to be applied:
   // that wave runs the whole pipeline with no token (every input load reads
@@ -279,10 +373,9 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 
   const int li = lane & 15, ls = lane >> 4;  // MFMA row / column index and k-slot
 
-  // ---- 1. small loads first: k/q chunks, gates, v of the lane's rows ----
+  // ---- 2. small loads first: k/q chunks, v of the lane's rows ----
   constexpr int C4 = KP / 4;  // 4-element chunks per vector
   constexpr int STAGE_PASSES = (NV * C4 + kVerifyThreads - 1) / kVerifyThreads;
-  constexpr int AS = int(sizeof(A));
   // DEFER: the pending commit's keys (token t, element kk) for LDS, FP32 or
   // activation-typed records (one of the two loads reads out of range).
   constexpr int PK_PASSES = DEFER ? (QM * C4 + kVerifyThreads - 1) / kVerifyThreads : 1;
@@ -329,27 +422,6 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       for (int e = 0; e < 4; ++e) xs[p][e] = xq[e] + xk[e];
     }
   }
-  // Gates are wave-uniform: scalar loads of the dword holding each one (FP32,
-  // or the 16-bit value at its half), decoded after the state loads issue.
-  // Tokens outside the window read the first word of query_start_loc instead
-  // (always present; g and beta may be empty, hence null, when the launch has
-  // no token at all) and are discarded.
-  const int gsz = a.g_f32 ? 4 : AS, bsz = a.beta_f32 ? 4 : AS;
-  const uintptr_t any_word = reinterpret_cast<uintptr_t>(a.qsl);
-  uint32_t graw[QM], braw[QM];
-  int gsh[QM], bsh[QM];
-#pragma unroll
-  for (int t = 0; t < QM; ++t) {
-    const bool tv = (valid_mask >> t) & 1u;
-    const uintptr_t ga =
-        tv ? reinterpret_cast<uintptr_t>(a.g) + uintptr_t(((bos + t) * a.g_ts + hv) * gsz) : any_word;
-    const uintptr_t ba =
-        tv ? reinterpret_cast<uintptr_t>(a.beta) + uintptr_t(((bos + t) * a.beta_ts + hv) * bsz) : any_word;
-    gsh[t] = int(ga & 2) * 8;
-    bsh[t] = int(ba & 2) * 8;
-    graw[t] = scalar_word(ga);
-    braw[t] = scalar_word(ba);
-  }
   // v of the lane's row in each half; the second half is loaded later, after
   // the loads it must not wait behind.
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v, bos * a.v_ts * AS);
@@ -365,7 +437,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   };
   load_v(0);
 
-  // ---- 2. first two state blocks ----
+  // ---- 3. first two state blocks ----
   // Buffer loads: one resource per (slot, head) tile, a 32-bit per-lane offset
   // per chunk and the block step in soffset. Rows >= V lie past the resource's
   // extent and read as zero; chunks >= K get an out-of-range offset.
@@ -427,8 +499,9 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 #pragma unroll
   for (int t = 0; t < QM; ++t) {
     const bool tv = (valid_mask >> t) & 1u;
-    float gv = a.g_f32 ? __uint_as_float(graw[t]) : bits_to_f32<A>((graw[t] >> gsh[t]) & 0xffffu);
-    float bv = a.beta_f32 ? __uint_as_float(braw[t]) : bits_to_f32<A>((braw[t] >> bsh[t]) & 0xffffu);
+    const uint32_t graw = word_of(gw, t), braw = word_of(gw, QM + t);
+    float gv = a.g_f32 ? __uint_as_float(graw) : bits_to_f32<A>((graw >> gsh[t]) & 0xffffu);
+    float bv = a.beta_f32 ? __uint_as_float(braw) : bits_to_f32<A>((braw >> bsh[t]) & 0xffffu);
     if (a.gated) {
       // docs/reference/recoverssm_gdn_upstream.py:135-151
       const float x = gv + dtb;
@@ -441,7 +514,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     bet[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? bv : 0.0f)));
   }
 
-  // ---- 3. stage vectors and records ----
+  // ---- 4. stage vectors and records ----
   const bool rec_ok = b < a.record_rows;
   const bool key_writer = rec_ok && vt == 0 && (a.key_per_value_head || (hv % ratio) == 0);
   const int key_head = a.key_per_value_head ? hv : h;
@@ -482,14 +555,10 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         for (int e = 0; e < 4; ++e) pk_lds[t][kk + e] = pkx[p][e];
       }
     }
-    const uintptr_t dbase = reinterpret_cast<uintptr_t>(a.p_decay);
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
       const bool live = pend && t < pn;
-      const uintptr_t off =
-          live ? uintptr_t((int64_t(prow) * a.p_decay_rs + int64_t(hv) * a.p_decay_hs + int64_t(t) * a.p_decay_ts) * 4)
-               : 0;
-      pdec[t] = live ? __uint_as_float(scalar_word(dbase + off)) : 1.0f;
+      pdec[t] = live ? __uint_as_float(word_of(gw, 2 * QM + 5 + t)) : 1.0f;
     }
   }
   wave_lds_sync();
@@ -573,7 +642,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     wave_lds_sync();
   }
 
-  // ---- 4. Gram matrix k_s . m_j (8 lanes per dot product, DPP sum) ----
+  // ---- 5. Gram matrix k_s . m_j (8 lanes per dot product, DPP sum) ----
   {
     const int j8 = lane & 7;
     for (int d0 = 0; d0 < QM * NV; d0 += kVerifyThreads / 8) {
@@ -595,7 +664,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const bool col_live = li < NV;
   const int brow = li & (NV - 1);
 
-  // ---- 5. pipelined S_0 . [k, q~] on the matrix cores, recurrence per half ----
+  // ---- 6. pipelined S_0 . [k, q~] on the matrix cores, recurrence per half ----
   auto gemv_block = [&](int rb, const uint4 (&src)[J]) {
     asm volatile("" ::: "memory");  // re-read the B operands for every block
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -622,11 +691,27 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   const __amdgpu_buffer_rsrc_t rout = make_rsrc(a.out, (bos * a.out_ts + out_base) * (out_f32 ? 4 : AS));
   const __amdgpu_buffer_rsrc_t rcorr =
       make_rsrc(a.corr, (int64_t(b) * a.corr_rs + int64_t(hv) * a.corr_hs + row0) * 4);
-  auto recurrence = [&](int half) {
-    wave_lds_sync();  // d_lds (and, on the first half, gram_lds) complete
+  float res_c[2][QM], res_o[2][QM];  // corrections and outputs of the lane's row in each half
+  auto emit = [&](int half) {
     const int lrow = half * 64 + lane;
     int row_ok = row0 + lrow < V;
     asm volatile("" : "+v"(row_ok));  // per-lane offsets below, not branches
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const bool st = ((valid_mask >> t) & 1u) && row_ok;
+      const int oel = t * int(a.out_ts) + lrow;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res_o[half][t]), rout,
+                                            st && out_f32 ? oel * 4 : kOutOfRange, 0, GDN_V_POL_OUT);
+      if constexpr (sizeof(A) == 2)
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f32<A>(res_o[half][t])), rout,
+                                              st && !out_f32 ? oel * AS : kOutOfRange, 0, GDN_V_POL_OUT);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res_c[half][t]), rcorr,
+                                            st && rec_ok ? (t * a.corr_ts + lrow) * 4 : kOutOfRange, 0,
+                                            GDN_V_POL_REC);
+    }
+  };
+  auto recurrence = [&](int half) {
+    wave_lds_sync();  // d_lds (and, on the first half, gram_lds) complete
     float u[QM], wq[QM];
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
@@ -644,16 +729,10 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 #pragma unroll
         for (int j = t; j < QM; ++j) wq[j] = __builtin_fmaf(c, gram_lds[t][QM + j], d * wq[j]);
       }
-      const bool st = tv && row_ok;
-      const int oel = t * int(a.out_ts) + lrow;
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(wq[t]), rout, st && out_f32 ? oel * 4 : kOutOfRange,
-                                            0, 0);
-      if constexpr (sizeof(A) == 2)
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f32<A>(wq[t])), rout,
-                                              st && !out_f32 ? oel * AS : kOutOfRange, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(c), rcorr,
-                                            st && rec_ok ? (t * a.corr_ts + lrow) * 4 : kOutOfRange, 0, 0);
+      res_c[half][t] = c;
+      res_o[half][t] = wq[t];
     }
+    if (!GDN_V_STORE_END) emit(half);
     wave_lds_sync();  // d_lds may be overwritten by the next half
   };
 #pragma unroll
@@ -668,6 +747,10 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     // Every half runs its recurrence, also one past V (its rows store nothing):
     // skipping it would be a path without its stores.
     if ((rb + 2) % 4 == 0) recurrence((rb + 2) / 4 - 1);
+  }
+  if (GDN_V_STORE_END) {
+#pragma unroll
+    for (int half = 0; half < NRB / 4; ++half) emit(half);
   }
 }
 

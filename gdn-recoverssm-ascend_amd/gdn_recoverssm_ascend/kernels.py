@@ -1,24 +1,24 @@
-"""RecoverSSM for Gated DeltaNet on AMD Instinct MI355X (gfx950).
+"""Verify and single-context commit: the host side, on AMD Instinct MI355X.
 
-Host side of the verify and single-context commit path. The public names,
-argument meaning and error behaviour follow the reference plugin's
-``gdn_recoverssm_ascend/kernels.py`` so that its callers
-(``layer_patch._verify`` and the commit proxy) run unchanged:
+The public names, argument meaning and error behaviour are the reference
+plugin's ``gdn_recoverssm_ascend/kernels.py`` (its callers, ``layer_patch._verify``
+and the commit proxy, run unchanged); everything below them is this module's:
 
-* ``gdn_recoverssm_verify`` -- verify a speculative window from the read-only
-  checkpoint (reference kernels.py:700-928);
-* ``ReplayRecordBuffers`` / ``record_nbytes`` / ``record_geometry_bytes`` -- the
-  typed-SoA record layout and its byte accounting (kernels.py:166-294);
-* ``GDNRecoverSSMCommitContext`` -- per-layer address tables and the commit
-  (kernels.py:1399-2052): the plan and the fold in one launch
+* ``gdn_recoverssm_verify`` (reference kernels.py:700-928), with the gated
+  variant (gating and the q/k L2 norm fused in) and the deferred variant (the
+  previous step's fold applied by this verify);
+* ``ReplayRecordBuffers``, ``record_nbytes``, ``record_geometry_bytes``: the
+  typed record planes and their byte counts (kernels.py:166-294);
+* ``GDNRecoverSSMCommitContext`` (kernels.py:1399-2052): one commit context
+  per cache epoch. Its commit is the plan and the fold in one launch
   (``gdn_recoverssm_plan_fold``), then the conv compaction that reads the
   stored plan; ``commit_deferred`` plans now and leaves the fold to the next
-  verify (``gdn_recoverssm_verify_deferred``).
+  verify.
 
-Every launch goes to the hand-written HIP kernels of ``libgdn_recoverssm_hip.so``
-through its C ABI (``_native``). Validation happens before any launch and raises
-``ValueError("GDN RecoverSSM: ...")``; a failed launch raises ``RuntimeError``
-and is never retried.
+Arguments are checked by rule tables (``_rules``) before anything is launched
+and a violation raises ``ValueError("GDN RecoverSSM: ...")``; every launch is a
+``_LaunchSpec`` of a C entry point of ``libgdn_recoverssm_hip.so`` (``_native``)
+on the current stream, and a failed launch raises ``RuntimeError``.
 """
 
 from __future__ import annotations
@@ -27,11 +27,14 @@ import ctypes
 from collections import Counter
 from collections.abc import Sequence
 from dataclasses import dataclass, field, replace
+from functools import cached_property
 from typing import Any
 
 import torch
 
 from . import _native as N
+from ._rules import enforce, require
+from ._tables import LayerPages, check_layers, record_planes
 
 # vLLM's physical null page (vllm.v1.attention.backends.utils.NULL_BLOCK_ID).
 NULL_BLOCK_ID = 0
@@ -42,49 +45,39 @@ MAX_SPEC_QUERY_LEN = 8
 # Largest key dimension the verify / fold kernels are instantiated for.
 MAX_KEY_DIM = 256
 
+_FLOAT_TYPES = (torch.float32, torch.bfloat16, torch.float16)
+_INDEX_TYPES = (torch.int32, torch.int64)
+
 _COUNTS: Counter = Counter()
 
 
 def counts() -> dict:
-    """Launch counters per entry point (``verify``, ``plan``, ``conv``, ``fold``, ``plan_fold``, ``publish``);
-    ``prepared_<name>`` counts compile-only preparations."""
+    """Launches per entry point (``verify``, ``plan``, ``conv``, ``fold``,
+    ``plan_fold``, ``publish``); ``prepared_<name>`` counts compile-only
+    preparations."""
     return dict(_COUNTS)
 
 
-# ---------------------------------------------------------------------------
-# Validation helpers (reference kernels.py:143-163)
-# ---------------------------------------------------------------------------
-
-
-def _require(cond: bool, msg: str) -> None:
-    """Argument validation that raises ``ValueError`` before any kernel launch."""
-    if not cond:
-        raise ValueError(f"GDN RecoverSSM: {msg}")
-
-
-def _ptr_table(tensors: Sequence[torch.Tensor], device, offsets: Sequence[int] | None = None) -> torch.Tensor:
-    """int64 device table of data pointers (plus optional byte offsets).
-
-    Pointers with the top bit set are stored with their uint64 bit pattern.
-    """
-    ptrs = [t.data_ptr() + (offsets[i] if offsets else 0) for i, t in enumerate(tensors)]
-    ptrs = [p if p < (1 << 63) else p - (1 << 64) for p in ptrs]
-    return torch.tensor(ptrs, dtype=torch.int64, device=device)
+# Kept for the grouped module and older callers: one rule, checked on the spot.
+_require = require
 
 
 # ---------------------------------------------------------------------------
-# Record buffers (reference kernels.py:166-294)
+# Records (reference kernels.py:166-294)
 # ---------------------------------------------------------------------------
+
+
+def _key_dtype_ok(dtype) -> bool:
+    return dtype in _FLOAT_TYPES
 
 
 @dataclass(frozen=True)
 class ReplayRecordBuffers:
-    """Step-owned typed records; keys are shared by grouped value heads.
-
-    ``correction [rows, HV, Q, V]`` FP32, ``key [rows, H, Q, K]`` in the key
-    dtype (an already-normalised BF16/FP16 key keeps its exact input bits),
-    ``decay [rows, HV, Q]`` FP32.
-    """
+    """What one verify leaves for the commit, as three row-indexed planes:
+    ``correction [rows, HV, Q, V]`` and ``decay [rows, HV, Q]`` in FP32, and
+    ``key [rows, H, Q, K]`` in the key dtype, one key per key head (the value
+    heads of a GQA group share it). A BF16/FP16 key record holds the input
+    key's own bits, so it is only allowed for already-normalised keys."""
 
     correction: torch.Tensor
     key: torch.Tensor
@@ -92,6 +85,7 @@ class ReplayRecordBuffers:
 
     @property
     def shape(self) -> tuple[int, int, int, int]:
+        """The logical packed shape, (rows, HV, Q, V + K + 1)."""
         rows, heads, window, value_dim = self.correction.shape
         return (rows, heads, window, value_dim + self.key.shape[-1] + 1)
 
@@ -116,65 +110,42 @@ class ReplayRecordBuffers:
         return sum(t.numel() * t.element_size() for t in (self.correction, self.key, self.decay))
 
     @classmethod
-    def allocate(
-        cls,
-        rows: int,
-        num_value_heads: int,
-        num_key_heads: int,
-        window: int,
-        value_dim: int,
-        key_dim: int,
-        *,
-        device,
-        key_dtype=torch.float32,
-    ):
-        _require(
-            rows > 0
-            and num_key_heads > 0
-            and 0 < window <= MAX_SPEC_QUERY_LEN
-            and value_dim > 0
-            and key_dim > 0
-            and num_value_heads > 0
-            and num_value_heads % num_key_heads == 0,
-            "record head/row geometry is invalid",
-        )
-        _require(
-            key_dtype in (torch.float16, torch.bfloat16, torch.float32),
-            "record keys require FP16, BF16 or FP32",
-        )
-        return cls(
-            torch.zeros((rows, num_value_heads, window, value_dim), dtype=torch.float32, device=device),
-            torch.zeros((rows, num_key_heads, window, key_dim), dtype=key_dtype, device=device),
-            torch.zeros((rows, num_value_heads, window), dtype=torch.float32, device=device),
-        )
+    def allocate(cls, rows: int, num_value_heads: int, num_key_heads: int, window: int, value_dim: int,
+                 key_dim: int, *, device, key_dtype=torch.float32):
+        enforce((
+            ("record head/row geometry is invalid",
+             lambda: min(rows, num_value_heads, num_key_heads, value_dim, key_dim) > 0
+             and 0 < window <= MAX_SPEC_QUERY_LEN and num_value_heads % num_key_heads == 0),
+            ("record keys require FP16, BF16 or FP32", lambda: _key_dtype_ok(key_dtype)),
+        ))
+        planes = {
+            "correction": ((rows, num_value_heads, window, value_dim), torch.float32),
+            "key": ((rows, num_key_heads, window, key_dim), key_dtype),
+            "decay": ((rows, num_value_heads, window), torch.float32),
+        }
+        return cls(**{name: torch.zeros(shape, dtype=dt, device=device) for name, (shape, dt) in planes.items()})
 
 
 def record_nbytes(record: torch.Tensor | ReplayRecordBuffers) -> int:
-    return record.record_bytes if isinstance(record, ReplayRecordBuffers) else record.numel() * record.element_size()
+    if isinstance(record, ReplayRecordBuffers):
+        return record.record_bytes
+    return record.numel() * record.element_size()
 
 
-def record_geometry_bytes(
-    rows: int,
-    num_layers: int,
-    num_value_heads: int,
-    num_key_heads: int,
-    window: int,
-    key_dim: int,
-    value_dim: int,
-    key_dtype=torch.float32,
-) -> int:
-    """Physical bytes of one step's records, with deduplicated keys in their dtype."""
-    _require(
-        min(rows, num_layers, num_value_heads, num_key_heads, window, key_dim, value_dim) > 0,
-        "record geometry must be positive",
-    )
-    _require(num_value_heads % num_key_heads == 0, "value heads must be a multiple of key heads")
-    _require(
-        key_dtype in (torch.float16, torch.bfloat16, torch.float32),
-        "record keys require FP16, BF16 or FP32",
-    )
-    key_bytes = 4 if key_dtype == torch.float32 else 2
-    return rows * num_layers * window * (num_value_heads * value_dim * 4 + num_key_heads * key_dim * key_bytes + num_value_heads * 4)
+def record_geometry_bytes(rows: int, num_layers: int, num_value_heads: int, num_key_heads: int, window: int,
+                          key_dim: int, value_dim: int, key_dtype=torch.float32) -> int:
+    """Bytes of one step's typed records over all layers: per (row, layer,
+    token) an FP32 correction and decay per value head and one key per key
+    head in its dtype."""
+    enforce((
+        ("record geometry must be positive",
+         lambda: min(rows, num_layers, num_value_heads, num_key_heads, window, key_dim, value_dim) > 0),
+        ("value heads must be a multiple of key heads", lambda: num_value_heads % num_key_heads == 0),
+        ("record keys require FP16, BF16 or FP32", lambda: _key_dtype_ok(key_dtype)),
+    ))
+    key_bytes = torch.empty((), dtype=key_dtype).element_size()
+    per_token = num_value_heads * (value_dim + 1) * 4 + num_key_heads * key_dim * key_bytes
+    return rows * num_layers * window * per_token
 
 
 # ---------------------------------------------------------------------------
@@ -184,13 +155,11 @@ def record_geometry_bytes(
 
 @dataclass
 class _LaunchSpec:
-    """One HIP launch, built once and launched on the current stream.
-
-    ``launch()`` submits it; ``compile_only()`` checks that the AOT library is
-    loaded and the entry point exists without touching device memory (the
-    kernels are compiled ahead of time). ``name`` is the entry point
-    (``verify`` / ``plan`` / ``conv`` / ``fold`` / ``plan_fold`` / ``publish``).
-    """
+    """One launch of a C entry point, built once and launched on the current
+    stream. ``launch()`` submits it; ``compile_only()`` only checks that the
+    ahead-of-time library and its entry point are there (nothing is compiled
+    at run time and no device memory is touched). ``name`` is the entry point
+    (``verify`` / ``plan`` / ``conv`` / ``fold`` / ``plan_fold`` / ``publish``)."""
 
     name: str
     fn: Any
@@ -199,8 +168,7 @@ class _LaunchSpec:
     keepalive: tuple = field(default_factory=tuple)
 
     def launch(self) -> None:
-        stream = N.stream_handle(self.device)
-        status = self.fn(*self.args, stream)
+        status = self.fn(*self.args, N.stream_handle(self.device))
         N.check(status, self.name)
         _COUNTS[self.name] += 1
 
@@ -219,8 +187,176 @@ def _lib():
 # ---------------------------------------------------------------------------
 
 
-def _aligned16(t: torch.Tensor) -> bool:
-    return t.data_ptr() % 16 == 0
+class _VerifyCall:
+    """The tensors of one verify call and the sizes that follow from them.
+    Sizes are read lazily, so each rule only touches what the rules before it
+    have established."""
+
+    def __init__(self, g, beta, q, k, v, checkpoint, records, qsl, indices, window, normalized, out, gating):
+        self.g, self.beta, self.q, self.k, self.v = g, beta, q, k, v
+        self.checkpoint, self.records, self.qsl, self.indices = checkpoint, records, qsl, indices
+        self.window, self.normalized, self.out, self.gating = int(window), normalized, out, gating
+        self.typed = isinstance(records, ReplayRecordBuffers)
+
+    tokens = cached_property(lambda c: c.q.shape[1])
+    H = cached_property(lambda c: c.q.shape[2])
+    K = cached_property(lambda c: c.q.shape[3])
+    HV = cached_property(lambda c: c.v.shape[2])
+    V = cached_property(lambda c: c.v.shape[3])
+    rows = cached_property(lambda c: c.indices.shape[0])
+    g2 = cached_property(lambda c: c.g.reshape(c.tokens, c.HV))
+    beta2 = cached_property(lambda c: c.beta.reshape(c.tokens, c.HV))
+    planes = cached_property(lambda c: record_planes(c.records, c.V, c.K))
+
+    def tensors(self):
+        p = self.planes
+        return (self.k, self.v, self.g, self.beta, self.checkpoint, p.correction, p.key, p.decay, self.qsl,
+                self.indices)
+
+
+_ACTIVATION_RULES = (
+    ("q must have shape [1, tokens, heads, dim]", lambda c: c.q.ndim == 4 and c.q.shape[0] == 1),
+    ("q and k shapes differ", lambda c: c.k.shape == c.q.shape),
+    ("v must have shape [1, tokens, value heads, dim]",
+     lambda c: c.v.ndim == 4 and tuple(c.v.shape[:2]) == (1, c.tokens)),
+    ("value heads must be a positive multiple of the q/k heads", lambda c: 0 < c.H <= c.HV and c.HV % c.H == 0),
+    ("A_log and dt_bias need one entry per value head",
+     lambda c: c.gating is None or c.gating[0].shape[0] == c.gating[1].shape[0] == c.HV),
+    ("gate or beta shape is incompatible", lambda c: c.g.numel() == c.beta.numel() == c.tokens * c.HV),
+    ("gate and beta heads must be contiguous", lambda c: c.g2.stride(1) == 1 and c.beta2.stride(1) == 1),
+    (f"spec_query_len must be in [1, {MAX_SPEC_QUERY_LEN}]", lambda c: 0 < c.window <= MAX_SPEC_QUERY_LEN),
+    ("q and k heads must be contiguous", lambda c: all(t.stride(-1) == 1 and t.stride(-2) == c.K for t in (c.q, c.k))),
+    ("v heads must be contiguous", lambda c: c.v.stride(-1) == 1 and c.v.stride(-2) == c.V),
+    ("checkpoint must be four-dimensional", lambda c: c.checkpoint.ndim == 4),
+    ("checkpoint shape is incompatible", lambda c: tuple(c.checkpoint.shape[1:]) == (c.HV, c.V, c.K)),
+)
+
+_TYPED_RECORD_RULES = (
+    ("typed record geometry is incompatible",
+     lambda c: c.planes.correction.ndim == 4
+     and tuple(c.planes.correction.shape[1:]) == (c.HV, c.window, c.V)
+     and tuple(c.planes.key.shape) == (c.planes.correction.shape[0], c.H, c.window, c.K)
+     and tuple(c.planes.decay.shape) == (c.planes.correction.shape[0], c.HV, c.window)),
+    ("correction and decay records must remain FP32",
+     lambda c: c.planes.correction.dtype == c.planes.decay.dtype == torch.float32),
+    ("low-precision key records require already-normalized input dtype",
+     lambda c: _key_dtype_ok(c.planes.key.dtype)
+     and (c.planes.key.dtype == torch.float32 or (c.normalized and c.planes.key.dtype == c.k.dtype))),
+    ("typed record innermost dimensions must be contiguous",
+     lambda c: all(t.stride(-1) == 1 for t in (c.planes.correction, c.planes.key, c.planes.decay))),
+)
+
+_PACKED_RECORD_RULES = (
+    ("packed replay record shape is incompatible",
+     lambda c: c.records.ndim == 4 and tuple(c.records.shape[1:]) == (c.HV, c.window, c.V + c.K + 1)),
+    ("packed records must remain FP32", lambda c: c.records.dtype == torch.float32),
+    ("packed record elements must be contiguous", lambda c: c.records.stride(-1) == 1),
+)
+
+_BATCH_RULES = (
+    ("replay buffer has no rows", lambda c: c.planes.correction.shape[0] >= 1),
+    ("state indices must be one-dimensional", lambda c: c.indices.ndim == 1),
+    ("query metadata is incompatible", lambda c: c.qsl.ndim == 1 and c.qsl.shape[0] == c.rows + 1),
+    ("speculative decode input exceeds its activation capacity", lambda c: c.tokens <= c.rows * c.window),
+    ("inputs must be on the same device",
+     lambda c: all(t.device == c.q.device for t in c.tensors()) and (c.out is None or c.out.device == c.q.device)),
+)
+
+
+def _kernel_rules(c: _VerifyCall) -> tuple:
+    """What the gfx950 kernels are built for (checked when there is work)."""
+    named = (("activation", c.q), ("output", c.out), ("gate", c.g2), ("beta", c.beta2), ("checkpoint", c.checkpoint))
+    chunk = 16 // c.checkpoint.element_size()
+    return (
+        ("q, k and v must share one activation dtype", lambda: c.q.dtype == c.k.dtype == c.v.dtype),
+        *((f"{name} dtype {t.dtype} is not supported", lambda t=t: t.dtype in _FLOAT_TYPES) for name, t in named),
+        ("query offsets and state indices must be int32 or int64",
+         lambda: c.qsl.dtype in _INDEX_TYPES and c.indices.dtype in _INDEX_TYPES),
+        ("verify runs on a HIP device", lambda: c.q.device.type == "cuda"),
+        (f"checkpoint rows must be contiguous, 16-byte aligned and K <= {MAX_KEY_DIM} a multiple of {chunk}",
+         lambda: c.K <= MAX_KEY_DIM and c.K % chunk == 0 and c.checkpoint.stride(3) == 1
+         and all(s % chunk == 0 for s in c.checkpoint.stride()[:3]) and c.checkpoint.data_ptr() % 16 == 0),
+    )
+
+
+def _check_verify(c: _VerifyCall) -> None:
+    enforce(_ACTIVATION_RULES, c)
+    enforce(_TYPED_RECORD_RULES if c.typed else _PACKED_RECORD_RULES, c)
+    enforce(_BATCH_RULES, c)
+
+
+def _verify_config(c: _VerifyCall, out: torch.Tensor) -> tuple:
+    """The 28 integer fields of the reference's GDN_VERIFY_FIELDS
+    (csrc/common.h:8-36), in their order."""
+    p = c.planes
+    # Packed records: the key and decay planes share the correction's strides.
+    key_strides = p.key.stride()[:3]
+    decay_strides = p.decay.stride()[:3]
+    return (c.rows, c.tokens, c.H, c.HV, c.window, c.checkpoint.shape[0], p.correction.shape[0], NULL_BLOCK_ID,
+            c.q.stride(1), c.k.stride(1), c.v.stride(1), c.g2.stride(0), c.beta2.stride(0),
+            *c.checkpoint.stride()[:3], *p.correction.stride()[:3], *key_strides, *decay_strides,
+            out.stride(1), c.qsl.stride(0), c.indices.stride(0))
+
+
+def _verify_spec(c: _VerifyCall, out, scale, *, pending=None) -> _LaunchSpec:
+    p = c.planes
+    config = _verify_config(c, out)
+    ext = N.VerifyExt(
+        key_dim=c.K, value_dim=c.V, act_dtype=N.dtype_code(c.q.dtype), beta_dtype=N.dtype_code(c.beta2.dtype),
+        g_dtype=N.dtype_code(c.g2.dtype), state_dtype=N.dtype_code(c.checkpoint.dtype),
+        key_record_dtype=N.dtype_code(torch.float32 if p.packed else p.key.dtype),
+        qsl_dtype=N.dtype_code(c.qsl.dtype), index_dtype=N.dtype_code(c.indices.dtype),
+        qk_l2norm=0 if c.normalized else 1, key_per_value_head=1 if p.packed else 0,
+        out_dtype=N.dtype_code(out.dtype),
+    )
+    cfg = N.i64_array(config)
+    lib = _lib()
+    inputs = (c.q.data_ptr(), c.k.data_ptr(), c.v.data_ptr(), c.g2.data_ptr(), c.beta2.data_ptr())
+    common = (c.checkpoint.data_ptr(), p.correction.data_ptr(), p.key.data_ptr() + p.key_offset,
+              p.decay.data_ptr() + p.decay_offset, out.data_ptr(), c.qsl.data_ptr(), c.indices.data_ptr(), cfg,
+              N.VERIFY_CONFIG_FIELDS, float(scale), ctypes.byref(ext))
+    keep = (c.q, c.k, c.v, c.g2, c.beta2, c.checkpoint, p.correction, p.key, p.decay, out, c.qsl, c.indices, cfg, ext)
+    if pending is not None:
+        struct, held = pending
+        fn, args = lib.gdn_recoverssm_verify_deferred, inputs + common + (ctypes.byref(struct),)
+        keep += (struct, held)
+    elif c.gating is None:
+        fn, args = lib.gdn_recoverssm_verify, inputs + common
+    else:
+        a_log, dt_bias, sp_beta, sp_threshold = c.gating
+        require(a_log.device == dt_bias.device == c.q.device, "inputs must be on the same device")
+        gext = N.GatingExt(a_log_dtype=N.dtype_code(a_log.dtype), dt_bias_dtype=N.dtype_code(dt_bias.dtype),
+                           softplus_beta=sp_beta, softplus_threshold=sp_threshold)
+        fn = lib.gdn_recoverssm_verify_gated
+        args = inputs + (a_log.data_ptr(), dt_bias.data_ptr()) + common + (ctypes.byref(gext),)
+        keep += (a_log, dt_bias, gext)
+    spec = _LaunchSpec("verify", fn, args, c.q.device, keepalive=keep)
+    spec.config = tuple(int(x) for x in config)
+    spec.scale = float(scale)
+    return spec
+
+
+def _run_verify(c: _VerifyCall, scale, out, _collect, *, pending=None) -> torch.Tensor:
+    """Checks, output allocation, the early return on an empty batch, the
+    kernel checks, then the launch (or its spec into ``_collect``)."""
+    _check_verify(c)
+    if scale is None:
+        scale = c.K ** -0.5
+    if out is None:
+        out = torch.empty(1, c.tokens, c.HV, c.V, dtype=c.v.dtype, device=c.v.device)
+    require(tuple(out.shape) == (1, c.tokens, c.HV, c.V) and out.stride()[2:] == (c.V, 1),
+            "output shape or layout is incompatible")
+    # Nothing to verify: done, unless pending commits still have to be applied.
+    if c.rows == 0 or (c.tokens == 0 and pending is None):
+        return out
+    c.out = out
+    enforce(_kernel_rules(c))
+    spec = _verify_spec(c, out, scale, pending=pending)
+    if _collect is None:
+        spec.launch()
+    else:
+        _collect.append(spec)
+    return out
 
 
 def gdn_recoverssm_verify(
@@ -240,17 +376,21 @@ def gdn_recoverssm_verify(
     out: torch.Tensor | None = None,
     _collect: list | None = None,
 ) -> torch.Tensor:
-    """Verify a GDN speculative window against its checkpoint without modifying it.
+    """Verify a speculative window from each row's checkpoint page, which is
+    only read (reference kernels.py:700-928).
 
-    ``g`` (log-space decay) and ``beta`` in shape [1, T, HV] or [T, HV]; q, k:
-    [1, T, H, K]; v: [1, T, HV, V]; checkpoint_state: [blocks, HV, V, K];
-    replay_cache: typed ``ReplayRecordBuffers`` or a packed FP32
-    [rows, HV, spec_query_len, V + K + 1] tensor. Returns out [1, T, HV, V].
-    Reference: kernels.py:700-928.
+    ``g`` (log decay) and ``beta``: [1, T, HV] or [T, HV]; ``q``, ``k``:
+    [1, T, H, K]; ``v``: [1, T, HV, V]; ``checkpoint_state``: [pages, HV, V, K];
+    ``replay_cache``: ``ReplayRecordBuffers`` or a packed FP32
+    [rows, HV, spec_query_len, V + K + 1] tensor; ``query_start_loc`` [B + 1];
+    ``state_indices`` [B] (a page <= 0 or past the pool is the null page: zero
+    outputs, no records). ``scale`` defaults to K^-0.5. With
+    ``qk_already_normalized=False`` q and k are L2-normalised in the kernel
+    (eps 1e-6). Returns ``out`` [1, T, HV, V], allocated when not given.
     """
-    return _verify(g, beta, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
-                   query_start_loc=query_start_loc, state_indices=state_indices, spec_query_len=spec_query_len,
-                   scale=scale, qk_already_normalized=qk_already_normalized, out=out, gating=None, _collect=_collect)
+    c = _VerifyCall(g, beta, q, k, v, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
+                    qk_already_normalized, out, None)
+    return _run_verify(c, scale, out, _collect)
 
 
 def gdn_recoverssm_verify_gated(
@@ -274,24 +414,31 @@ def gdn_recoverssm_verify_gated(
     out: torch.Tensor | None = None,
     _collect: list | None = None,
 ) -> torch.Tensor:
-    """Verify with the gating producer (and, by default, the q/k L2 norm)
-    fused in, as the gated verify of docs/reference/recoverssm_gdn_upstream.py:83-151.
+    """Verify with the layer's gating producer (and by default the q/k L2
+    norm) computed in the kernel, as the gated verify of
+    docs/reference/recoverssm_gdn_upstream.py:83-151.
 
-    ``a`` and ``b`` are the raw gate projections ([1, T, HV] or [T, HV]);
-    ``A_log`` and ``dt_bias`` are [HV]. Inside the kernel, in FP32:
-    g = -exp(A_log) * softplus(a + dt_bias) (softplus with ``softplus_beta``
-    and ``softplus_threshold``, as vLLM's fused_gdn_gating) and
-    beta = sigmoid(b). q and k are raw unless ``qk_already_normalized``. It
-    replaces the producers the layer runs before verify
+    ``a``, ``b``: the raw gate projections ([1, T, HV] or [T, HV]); ``A_log``,
+    ``dt_bias``: [HV]. Per token and value head, in FP32:
+    g = -exp(A_log) * softplus(a + dt_bias) with vLLM's fused_gdn_gating
+    softplus (``softplus_beta``, ``softplus_threshold``), and beta = sigmoid(b).
+    It replaces the producers the layer runs before verify
     (spec_forward.py:91-96) and their round trip through memory.
     """
-    _require(A_log.ndim == 1 and dt_bias.ndim == 1, "A_log and dt_bias must be one-dimensional")
-    _require(A_log.stride(0) == 1 and dt_bias.stride(0) == 1, "A_log and dt_bias must be contiguous")
-    _require(float(softplus_beta) > 0.0, "softplus beta must be positive")
-    return _verify(a, b, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
-                   query_start_loc=query_start_loc, state_indices=state_indices, spec_query_len=spec_query_len,
-                   scale=scale, qk_already_normalized=qk_already_normalized, out=out,
-                   gating=(A_log, dt_bias, float(softplus_beta), float(softplus_threshold)), _collect=_collect)
+    enforce((
+        ("A_log and dt_bias must be one-dimensional", lambda: A_log.ndim == 1 and dt_bias.ndim == 1),
+        ("A_log and dt_bias must be contiguous", lambda: A_log.stride(0) == 1 and dt_bias.stride(0) == 1),
+        ("softplus beta must be positive", lambda: float(softplus_beta) > 0.0),
+    ))
+    gating = (A_log, dt_bias, float(softplus_beta), float(softplus_threshold))
+    c = _VerifyCall(a, b, q, k, v, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
+                    qk_already_normalized, out, gating)
+    return _run_verify(c, scale, out, _collect)
+
+
+# ---------------------------------------------------------------------------
+# Deferred commit
+# ---------------------------------------------------------------------------
 
 
 @dataclass
@@ -321,6 +468,10 @@ class PendingCommit:
     records: "ReplayRecordBuffers"
     num_rows: int = 0
 
+    @property
+    def plan(self) -> tuple:
+        return (self.source, self.lengths, self.final, self.boundary, self.boundary_len)
+
 
 def continue_pending(pending: Sequence[PendingCommit], previous_requests: Sequence, next_requests: Sequence):
     """Re-key one step's pending commits (one per layer) for the next batch.
@@ -333,23 +484,39 @@ def continue_pending(pending: Sequence[PendingCommit], previous_requests: Sequen
     is not in the next batch: their commits are applied by no verify, so
     ``flush_deferred(rows=...)`` must fold them before their pages are reused.
     """
-    _require(len(pending) > 0, "no pending commits to continue")
+    require(len(pending) > 0, "no pending commits to continue")
     num_rows = int(pending[0].num_rows)
-    _require(all(int(p.num_rows) == num_rows for p in pending), "pending commits of one step disagree on their rows")
-    _require(len(previous_requests) >= num_rows, "previous request ids do not cover the pending rows")
+    require(all(int(p.num_rows) == num_rows for p in pending), "pending commits of one step disagree on their rows")
+    require(len(previous_requests) >= num_rows, "previous request ids do not cover the pending rows")
     where = {}
     for r, req in enumerate(previous_requests[:num_rows]):
-        _require(req not in where, f"request {req!r} appears twice in the pending step")
+        require(req not in where, f"request {req!r} appears twice in the pending step")
         where[req] = r
     seen = set()
     mapping = []
     for req in next_requests:
-        _require(req not in seen, f"request {req!r} appears twice in the next batch")
+        require(req not in seen, f"request {req!r} appears twice in the next batch")
         seen.add(req)
         mapping.append(where.get(req, -1))
     left = sorted(r for req, r in where.items() if req not in seen)
     rows = torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=pending[0].rows.device)
     return tuple(replace(p, rows=rows) for p in pending), left
+
+
+_PENDING_RULES = (
+    ("the deferred commit needs typed record buffers",
+     lambda p, recs: isinstance(p.records, ReplayRecordBuffers) and isinstance(recs, ReplayRecordBuffers)),
+    ("the pending commit's records must not be the records this verify writes",
+     lambda p, recs: p.records.correction.data_ptr() != recs.correction.data_ptr()),
+    ("pending arrays must be contiguous one-dimensional int32",
+     lambda p, recs: all(t.dtype == torch.int32 and t.ndim == 1 and t.stride(0) == 1 for t in (p.rows,) + p.plan)),
+    ("pending plan arrays do not cover their rows",
+     lambda p, recs: all(t.shape[0] >= int(p.num_rows) for t in p.plan)),
+    ("the pending plan has more rows than its records", lambda p, recs: int(p.num_rows) <= p.records.correction.shape[0]),
+    ("pending records do not match this layer's record geometry",
+     lambda p, recs: p.records.correction.shape[1:] == recs.correction.shape[1:]
+     and p.records.key.shape[1:] == recs.key.shape[1:]),
+)
 
 
 def gdn_recoverssm_verify_deferred(
@@ -383,241 +550,124 @@ def gdn_recoverssm_verify_deferred(
     applies stay pending (see ``continue_pending`` and ``flush_deferred``).
     With no token in the batch the launch still applies the pending commits.
     """
-    rec = pending.records
-    _require(isinstance(rec, ReplayRecordBuffers), "the deferred commit needs typed record buffers")
-    _require(isinstance(replay_cache, ReplayRecordBuffers), "the deferred commit needs typed record buffers")
-    _require(
-        rec.correction.data_ptr() != replay_cache.correction.data_ptr(),
-        "the pending commit's records must not be the records this verify writes",
-    )
-    batch = state_indices.shape[0]
-    num_rows = int(pending.num_rows)
-    if num_rows <= 0:
+    enforce(_PENDING_RULES, pending, replay_cache)
+    if int(pending.num_rows) <= 0:
         # Nothing is pending: the ordinary verify.
         return gdn_recoverssm_verify(g, beta, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
                                      query_start_loc=query_start_loc, state_indices=state_indices,
                                      spec_query_len=spec_query_len, scale=scale,
                                      qk_already_normalized=qk_already_normalized, out=out, _collect=_collect)
-    plan = (pending.source, pending.lengths, pending.final, pending.boundary, pending.boundary_len)
-    _require(
-        all(t_.dtype == torch.int32 and t_.ndim == 1 and t_.stride(0) == 1 for t_ in (pending.rows,) + plan),
-        "pending arrays must be contiguous one-dimensional int32",
-    )
-    _require(pending.rows.shape[0] >= batch, "the pending row map does not cover the batch")
-    _require(all(t_.shape[0] >= num_rows for t_ in plan), "pending plan arrays do not cover their rows")
-    _require(num_rows <= rec.correction.shape[0], "the pending plan has more rows than its records")
-    _require(
-        rec.correction.shape[1:] == replay_cache.correction.shape[1:] and rec.key.shape[1:] == replay_cache.key.shape[1:],
-        "pending records do not match this layer's record geometry",
-    )
-    arrays = (pending.rows,) + plan
-    pc = N.PendingCommit(
-        rows=arrays[0].data_ptr(), source=arrays[1].data_ptr(), lengths=arrays[2].data_ptr(),
-        final_indices=arrays[3].data_ptr(), boundary_indices=arrays[4].data_ptr(),
-        boundary_lengths=arrays[5].data_ptr(), correction=rec.correction.data_ptr(), key=rec.key.data_ptr(),
-        decay=rec.decay.data_ptr(), record_rows=rec.correction.shape[0],
-        key_dtype=N.dtype_code(rec.key.dtype), key_per_value_head=0, num_rows=num_rows,
+    require(pending.rows.shape[0] >= state_indices.shape[0], "the pending row map does not cover the batch")
+    rec = pending.records
+    struct = N.PendingCommit(
+        rows=pending.rows.data_ptr(), source=pending.source.data_ptr(), lengths=pending.lengths.data_ptr(),
+        final_indices=pending.final.data_ptr(), boundary_indices=pending.boundary.data_ptr(),
+        boundary_lengths=pending.boundary_len.data_ptr(), correction=rec.correction.data_ptr(),
+        key=rec.key.data_ptr(), decay=rec.decay.data_ptr(), record_rows=rec.correction.shape[0],
+        key_dtype=N.dtype_code(rec.key.dtype), key_per_value_head=0, num_rows=int(pending.num_rows),
     )
     for i in range(3):
-        pc.corr_strides[i] = rec.correction.stride(i)
-        pc.key_strides[i] = rec.key.stride(i)
-        pc.decay_strides[i] = rec.decay.stride(i)
-    return _verify(g, beta, q, k, v, checkpoint_state=checkpoint_state, replay_cache=replay_cache,
-                   query_start_loc=query_start_loc, state_indices=state_indices, spec_query_len=spec_query_len,
-                   scale=scale, qk_already_normalized=qk_already_normalized, out=out, gating=None,
-                   pending=(pc, arrays, rec), _collect=_collect)
+        struct.corr_strides[i] = rec.correction.stride(i)
+        struct.key_strides[i] = rec.key.stride(i)
+        struct.decay_strides[i] = rec.decay.stride(i)
+    c = _VerifyCall(g, beta, q, k, v, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
+                    qk_already_normalized, out, None)
+    return _run_verify(c, scale, out, _collect, pending=(struct, (pending, rec)))
 
 
-def _verify(g, beta, q, k, v, *, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
-            scale, qk_already_normalized, out, gating, _collect, pending=None):
-    _require(q.ndim == 4 and q.shape[0] == 1, "q must have shape [1, tokens, heads, dim]")
-    _, total, H, K = q.shape
-    _require(k.shape == q.shape, "q and k shapes differ")
-    _require(v.ndim == 4 and tuple(v.shape[:2]) == (1, total), "v must have shape [1, tokens, value heads, dim]")
-    HV, V = v.shape[-2], v.shape[-1]
-    _require(H > 0 and HV >= H and HV % H == 0, "value heads must be a positive multiple of the q/k heads")
-    if gating is not None:
-        _require(gating[0].shape[0] == HV and gating[1].shape[0] == HV, "A_log and dt_bias need one entry per value head")
-    _require(g.numel() == total * HV and beta.numel() == total * HV, "gate or beta shape is incompatible")
-    g2 = g.reshape(total, HV)
-    beta2 = beta.reshape(total, HV)
-    _require(g2.stride(1) == 1 and beta2.stride(1) == 1, "gate and beta heads must be contiguous")
-    _require(0 < spec_query_len <= MAX_SPEC_QUERY_LEN, f"spec_query_len must be in [1, {MAX_SPEC_QUERY_LEN}]")
-    _require(all(t_.stride(-1) == 1 and t_.stride(-2) == K for t_ in (q, k)), "q and k heads must be contiguous")
-    _require(v.stride(-1) == 1 and v.stride(-2) == V, "v heads must be contiguous")
-    _require(checkpoint_state.ndim == 4, "checkpoint must be four-dimensional")
-    nb = checkpoint_state.shape[0]
-    _require(tuple(checkpoint_state.shape[1:]) == (HV, V, K), "checkpoint shape is incompatible")
-    soa = isinstance(replay_cache, ReplayRecordBuffers)
-    if soa:
-        corr, key_record, decay_record = replay_cache.correction, replay_cache.key, replay_cache.decay
-        _require(
-            corr.ndim == 4
-            and tuple(corr.shape[1:]) == (HV, spec_query_len, V)
-            and tuple(key_record.shape) == (corr.shape[0], H, spec_query_len, K)
-            and tuple(decay_record.shape) == (corr.shape[0], HV, spec_query_len),
-            "typed record geometry is incompatible",
-        )
-        _require(corr.dtype == decay_record.dtype == torch.float32, "correction and decay records must remain FP32")
-        _require(
-            key_record.dtype in (torch.float16, torch.bfloat16, torch.float32)
-            and (key_record.dtype == torch.float32 or (qk_already_normalized and key_record.dtype == k.dtype)),
-            "low-precision key records require already-normalized input dtype",
-        )
-        _require(
-            all(t.stride(-1) == 1 for t in (corr, key_record, decay_record)),
-            "typed record innermost dimensions must be contiguous",
-        )
+# ---------------------------------------------------------------------------
+# Commit launches shared by the single context and the grouped buckets
+# ---------------------------------------------------------------------------
+
+
+def _fill_plan_group(group, *, state_indices, query_start_loc, request_indices, block_table, num_computed_tokens,
+                     block_size, num_blocks) -> None:
+    """One gdn_plan_group: the step metadata of one cache group (grouped_commit.py:113-146)."""
+    def bind(t, ptr, stride, dtype):
+        setattr(group, ptr, t.data_ptr())
+        setattr(group, stride, t.stride(0))
+        setattr(group, dtype, N.dtype_code(t.dtype))
+
+    bind(state_indices, "state_indices", "si_stride", "si_dtype")
+    bind(query_start_loc, "query_start_loc", "qsl_stride", "qsl_dtype")
+    if request_indices is not None:
+        bind(request_indices, "request_indices", "map_stride", "map_dtype")
+    if block_table is not None:
+        group.block_table = block_table.data_ptr()
+        group.table_row_stride, group.table_col_stride = block_table.stride()
+        group.table_rows, group.table_width = block_table.shape
+        group.table_dtype = N.dtype_code(block_table.dtype)
+        bind(num_computed_tokens, "num_computed", "computed_stride", "computed_dtype")
+        group.computed_len = num_computed_tokens.shape[0]
+        group.block_size = int(block_size)
     else:
-        corr = key_record = decay_record = replay_cache
-        _require(
-            corr.ndim == 4 and tuple(corr.shape[1:]) == (HV, spec_query_len, V + K + 1),
-            "packed replay record shape is incompatible",
-        )
-        _require(corr.dtype == torch.float32, "packed records must remain FP32")
-        _require(corr.stride(-1) == 1, "packed record elements must be contiguous")
-    _require(corr.shape[0] >= 1, "replay buffer has no rows")
-    _require(state_indices.ndim == 1, "state indices must be one-dimensional")
-    _require(
-        query_start_loc.ndim == 1 and query_start_loc.shape[0] == state_indices.shape[0] + 1,
-        "query metadata is incompatible",
-    )
-    _require(total <= state_indices.shape[0] * spec_query_len, "speculative decode input exceeds its activation capacity")
-    _dev = q.device
-    _require(
-        all(
-            t_.device == _dev
-            for t_ in (k, v, g, beta, checkpoint_state, corr, key_record, decay_record, query_start_loc, state_indices)
-            if t_ is not None
-        )
-        and (out is None or out.device == _dev),
-        "inputs must be on the same device",
-    )
-    if scale is None:
-        scale = K**-0.5
-    if out is None:
-        out = torch.empty(1, total, HV, V, dtype=v.dtype, device=v.device)
-    _require(tuple(out.shape) == (1, total, HV, V) and out.stride()[2:] == (V, 1), "output shape or layout is incompatible")
-    batch = state_indices.shape[0]
-    if batch == 0 or (total == 0 and pending is None):
-        return out
-    # What the gfx950 kernels are built for (checked before any launch).
-    _require(q.dtype == k.dtype == v.dtype, "q, k and v must share one activation dtype")
-    for name, t_ in (("activation", q), ("output", out), ("gate", g2), ("beta", beta2), ("checkpoint", checkpoint_state)):
-        _require(t_.dtype in (torch.float32, torch.bfloat16, torch.float16), f"{name} dtype {t_.dtype} is not supported")
-    _require(
-        query_start_loc.dtype in (torch.int32, torch.int64) and state_indices.dtype in (torch.int32, torch.int64),
-        "query offsets and state indices must be int32 or int64",
-    )
-    _require(_dev.type == "cuda", "verify runs on a HIP device")
-    es = checkpoint_state.element_size()
-    chunk = 16 // es
-    _require(
-        K <= MAX_KEY_DIM
-        and K % chunk == 0
-        and checkpoint_state.stride(3) == 1
-        and all(s_ % chunk == 0 for s_ in checkpoint_state.stride()[:3])
-        and _aligned16(checkpoint_state),
-        f"checkpoint rows must be contiguous, 16-byte aligned and K <= {MAX_KEY_DIM} a multiple of {chunk}",
-    )
-    f32 = 4
-    if soa:
-        key_ptr, decay_ptr = key_record.data_ptr(), decay_record.data_ptr()
-        key_strides = key_record.stride()[:3]
-        decay_strides = decay_record.stride()
-        key_dtype = key_record.dtype
-        key_per_value_head = 0
-    else:
-        # Packed [corr(V) | key(K) | decay(1)] FP32 rows: the key and decay
-        # planes are views into the same record at offsets V and V + K.
-        key_ptr = corr.data_ptr() + V * f32
-        decay_ptr = corr.data_ptr() + (V + K) * f32
-        key_strides = corr.stride()[:3]
-        decay_strides = corr.stride()[:3]
-        key_dtype = torch.float32
-        key_per_value_head = 1
-    config = (
-        batch,
-        total,
-        H,
-        HV,
-        spec_query_len,
-        nb,
-        corr.shape[0],
-        NULL_BLOCK_ID,
-        q.stride(1),
-        k.stride(1),
-        v.stride(1),
-        g2.stride(0),
-        beta2.stride(0),
-        checkpoint_state.stride(0),
-        checkpoint_state.stride(1),
-        checkpoint_state.stride(2),
-        corr.stride(0),
-        corr.stride(1),
-        corr.stride(2),
-        *key_strides,
-        *decay_strides,
-        out.stride(1),
-        query_start_loc.stride(0),
-        state_indices.stride(0),
-    )
-    ext = N.VerifyExt(
-        key_dim=K,
-        value_dim=V,
-        act_dtype=N.dtype_code(q.dtype),
-        beta_dtype=N.dtype_code(beta2.dtype),
-        g_dtype=N.dtype_code(g2.dtype),
-        state_dtype=N.dtype_code(checkpoint_state.dtype),
-        key_record_dtype=N.dtype_code(key_dtype),
-        qsl_dtype=N.dtype_code(query_start_loc.dtype),
-        index_dtype=N.dtype_code(state_indices.dtype),
-        qk_l2norm=0 if qk_already_normalized else 1,
-        key_per_value_head=key_per_value_head,
-        out_dtype=N.dtype_code(out.dtype),
-    )
+        group.block_size = 1
+        group.table_width = 1
+    group.num_blocks = int(num_blocks)
+
+
+def _conv_spec(pages: LayerPages, *, source, source_dtype, source_stride, plan, layer_groups, capacity, rows,
+               history, max_blocks, align, device, keep=()) -> _LaunchSpec:
+    conv = pages.conv_states[0]
+    require(conv.element_size() in (2, 4), "conv state elements must be 2 or 4 bytes")
+    lengths, finals, boundaries, boundary_lens = plan
+    args = (pages.conv_addrs.data_ptr(), pages.conv_block_strides.data_ptr(), pages.conv_dim_strides.data_ptr(),
+            pages.conv_token_strides.data_ptr(), source.data_ptr(), source_dtype, source_stride, lengths.data_ptr(),
+            finals.data_ptr(), boundaries.data_ptr(), boundary_lens.data_ptr(),
+            None if layer_groups is None else layer_groups.data_ptr(), capacity, NULL_BLOCK_ID, rows,
+            len(pages.conv_states), conv.shape[1], history, conv.shape[2], max_blocks, conv.element_size(),
+            1 if align else 0)
+    return _LaunchSpec("conv", _lib().gdn_recoverssm_conv_compact, args, device, keepalive=keep)
+
+
+def _make_fold_spec(*, pages: LayerPages, record_rows, key_heads, key_dtype, rows, plan_capacity, num_blocks,
+                    spec_query_len, layer_groups, source, plan) -> _LaunchSpec:
+    """The fold launch (config = the 17 GDN_FOLD_FIELDS of csrc/common.h:37-54)."""
+    ref = pages.checkpoints[0]
+    _, HV, V, K = ref.shape
+    chunk = 16 // ref.element_size()
+    planes = pages.first_planes
+    enforce((
+        ("checkpoint dtype is not supported", lambda: ref.dtype in _FLOAT_TYPES),
+        ("record key dtype is not supported", lambda: key_dtype in _FLOAT_TYPES),
+        (f"checkpoint rows must be contiguous, 16-byte aligned, K <= {MAX_KEY_DIM} a multiple of {chunk}, V <= 1024",
+         lambda: K <= MAX_KEY_DIM and K % chunk == 0 and ref.stride(3) == 1
+         and all(s % chunk == 0 for s in ref.stride()[:3]) and V <= 1024),
+    ))
+    config = (rows, len(pages.checkpoints), HV, key_heads, spec_query_len, num_blocks, record_rows, plan_capacity,
+              NULL_BLOCK_ID, ref.stride(1), ref.stride(2), *planes.correction.stride()[1:3], *planes.key.stride()[1:3],
+              *planes.decay.stride()[1:3])
+    ext = N.FoldExt(key_dim=K, value_dim=V, state_dtype=N.dtype_code(ref.dtype), key_dtype=N.dtype_code(key_dtype),
+                    source_dtype=N.dtype_code(source.dtype), reserved=0, source_stride=source.stride(0),
+                    state_k_stride=ref.stride(3))
     cfg = N.i64_array(config)
-    lib = _lib()
-    tail = (
-        checkpoint_state.data_ptr(),
-        corr.data_ptr(),
-        key_ptr,
-        decay_ptr,
-        out.data_ptr(),
-        query_start_loc.data_ptr(),
-        state_indices.data_ptr(),
-        cfg,
-        N.VERIFY_CONFIG_FIELDS,
-        float(scale),
-        ctypes.byref(ext),
-    )
-    keep = (q, k, v, g2, beta2, checkpoint_state, corr, key_record, decay_record, out, query_start_loc, state_indices,
-            cfg, ext)
-    if pending is not None:
-        pc, arrays, rec = pending
-        fn = lib.gdn_recoverssm_verify_deferred
-        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(), beta2.data_ptr()) + tail + (ctypes.byref(pc),)
-        keep = keep + (pc, arrays, rec)
-    elif gating is None:
-        fn, args = lib.gdn_recoverssm_verify, (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(),
-                                                beta2.data_ptr()) + tail
-    else:
-        a_log, dt_bias, sp_beta, sp_threshold = gating
-        _require(all(t_.device == _dev for t_ in (a_log, dt_bias)), "inputs must be on the same device")
-        gext = N.GatingExt(a_log_dtype=N.dtype_code(a_log.dtype), dt_bias_dtype=N.dtype_code(dt_bias.dtype),
-                           softplus_beta=sp_beta, softplus_threshold=sp_threshold)
-        fn = lib.gdn_recoverssm_verify_gated
-        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g2.data_ptr(), beta2.data_ptr(), a_log.data_ptr(),
-                dt_bias.data_ptr()) + tail + (ctypes.byref(gext),)
-        keep = keep + (a_log, dt_bias, gext)
-    spec = _LaunchSpec("verify", fn, args, _dev, keepalive=keep)
+    tables = pages.device_tables
+    args = (ref.data_ptr(), planes.correction.data_ptr(), planes.key.data_ptr(), planes.decay.data_ptr(),
+            *(t.data_ptr() for t in tables), None if layer_groups is None else layer_groups.data_ptr(),
+            source.data_ptr(), *(t.data_ptr() for t in plan), cfg, N.FOLD_CONFIG_FIELDS, ctypes.byref(ext))
+    spec = _LaunchSpec("fold", _lib().gdn_recoverssm_fold, args, ref.device,
+                       keepalive=(pages, layer_groups, source, *plan, cfg, ext))
     spec.config = tuple(int(x) for x in config)
-    spec.scale = float(scale)
-    if _collect is None:
-        spec.launch()
-    else:
-        _collect.append(spec)
-    return out
+    return spec
+
+
+# Positions in the fold's argument tuple: 4 reference tensors, 8 tables,
+# layer groups, source, 4 plan arrays, config, config length, extension.
+_FOLD_LENGTHS_ARG = 14
+_FOLD_PLAN_ARGS = slice(13, 18)
+
+
+def _fuse_plan_fold(plan: _LaunchSpec, fold: _LaunchSpec) -> _LaunchSpec:
+    """``gdn_recoverssm_plan_fold``: a plan launch and the fold launch that
+    reads its arrays as one launch with identical results (each fold
+    workgroup plans its own row; extra workgroups store the plan arrays)."""
+    launch = N.plan_launch(plan.args)
+    args = ((ctypes.byref(launch),) + tuple(fold.args[:_FOLD_PLAN_ARGS.start])
+            + tuple(fold.args[_FOLD_PLAN_ARGS.stop:]))
+    spec = _LaunchSpec("plan_fold", _lib().gdn_recoverssm_plan_fold, args, fold.device,
+                       keepalive=(plan.keepalive, fold.keepalive, launch))
+    spec.config = fold.config
+    return spec
 
 
 # ---------------------------------------------------------------------------
@@ -625,38 +675,75 @@ def _verify(g, beta, q, k, v, *, checkpoint_state, replay_cache, query_start_loc
 # ---------------------------------------------------------------------------
 
 
-def _record_planes(record, V: int, K: int):
-    """(correction, key, decay) tensors plus the byte offsets of key / decay.
+def _commit_rules(ctx, accepted, state_indices, qsl, request_indices, block_table, num_computed, block_size):
+    align_parts = (block_table, num_computed, block_size)
+    batch = state_indices.shape[0]
+    device = ctx.checkpoints[0].device
+    tensors = (accepted, state_indices, qsl, request_indices, block_table, num_computed)
+    return (
+        ("state indices must be one-dimensional", lambda: state_indices.ndim == 1),
+        ("commit batch exceeds its plan capacity", lambda: batch <= ctx.commit_lens.shape[0]),
+        ("commit metadata is incompatible", lambda: qsl.ndim == 1 and qsl.shape[0] == batch + 1),
+        ("request mapping is too short", lambda: request_indices is None or request_indices.shape[0] >= batch),
+        ("accepted-token counts are too short",
+         lambda: accepted.ndim == 1 and (request_indices is not None or accepted.shape[0] >= batch)),
+        ("align metadata is incomplete",
+         lambda: all(x is None for x in align_parts) or all(x is not None for x in align_parts)),
+        ("align block size must cover one speculative window",
+         lambda: block_size is None or block_size >= ctx.spec_query_len),
+        ("block table must be two-dimensional with a positive width",
+         lambda: block_table is None or (block_table.ndim == 2 and block_table.shape[1] > 0)),
+        ("commit inputs must be on the same device",
+         lambda: all(t is None or t.device == device for t in tensors)),
+        ("the commit runs on a HIP device", lambda: device.type == "cuda"),
+    )
 
-    Typed records expose three planes. A packed FP32 record [rows, HV, Q, V+K+1]
-    is addressed as three strided planes of the same storage: the key at
-    element offset V and the decay at V + K of every (row, head, token) record.
-    """
-    if isinstance(record, ReplayRecordBuffers):
-        return record.correction, record.key, record.decay, 0, 0
-    return record, record, record, V * 4, (V + K) * 4
 
-
-@dataclass
 class GDNRecoverSSMCommitContext:
-    conv_states: tuple
-    conv_state_base_addrs: torch.Tensor
-    conv_state_block_strides: torch.Tensor
-    conv_state_dim_strides: torch.Tensor
-    conv_state_token_strides: torch.Tensor
-    conv_history_len: int
-    checkpoints: tuple
-    state_base_addrs: torch.Tensor
-    state_block_strides: torch.Tensor
-    replays: tuple
-    replay_base_addrs: torch.Tensor
-    replay_block_strides: torch.Tensor
-    commit_lens: torch.Tensor
-    final_state_indices: torch.Tensor
-    boundary_state_indices: torch.Tensor
-    boundary_recovery_lens: torch.Tensor
-    spec_query_len: int
-    num_blocks: int
+    """The commit of one cache epoch: every layer's checkpoint pages, conv
+    states and record planes bound once (their device address tables built
+    once), and the plan arrays of up to ``max_num_reqs`` rows, reused by every
+    step. ``commit`` folds each row's accepted prefix into its final page (and
+    the align-mode boundary snapshot) and compacts the conv states."""
+
+    def __init__(self, pages: LayerPages, *, spec_query_len: int, max_num_reqs: int, conv_history_len: int,
+                 record_layout: str, num_key_heads: int, key_dtype):
+        self.pages = pages
+        self.spec_query_len = int(spec_query_len)
+        self.num_blocks = int(pages.checkpoints[0].shape[0])
+        self.conv_history_len = int(conv_history_len)
+        self.record_layout = record_layout
+        self.num_key_heads = int(num_key_heads)
+        self.key_dtype = key_dtype
+        self.records = list(pages.records)
+        self.record_rows = int(pages.first_planes.correction.shape[0])
+        self.record_bytes = sum(record_nbytes(r) for r in pages.records)
+        dev = pages.checkpoints[0].device
+        plan = {name: torch.zeros(max_num_reqs, dtype=torch.int32, device=dev) for name in (
+            "commit_lens", "final_state_indices", "boundary_state_indices", "boundary_recovery_lens", "align_valid",
+            "align_col", "plan_source")}
+        self.__dict__.update(plan)
+        # Rows of the next batch continue the same rows of a pending commit.
+        self.pending_rows = torch.arange(max_num_reqs, dtype=torch.int32, device=dev)
+
+    # The reference context's table attributes, served from the bound pages.
+    conv_states = property(lambda self: self.pages.conv_states)
+    checkpoints = property(lambda self: self.pages.checkpoints)
+    replays = property(lambda self: self.pages.records)
+    conv_state_base_addrs = property(lambda self: self.pages.conv_addrs)
+    conv_state_block_strides = property(lambda self: self.pages.conv_block_strides)
+    conv_state_dim_strides = property(lambda self: self.pages.conv_dim_strides)
+    conv_state_token_strides = property(lambda self: self.pages.conv_token_strides)
+    state_base_addrs = property(lambda self: self.pages.state_addrs)
+    state_block_strides = property(lambda self: self.pages.state_block_strides)
+    correction_base_addrs = property(lambda self: self.pages.correction_addrs)
+    correction_block_strides = property(lambda self: self.pages.correction_block_strides)
+    replay_base_addrs = correction_base_addrs
+    replay_block_strides = correction_block_strides
+    key_base_addrs = property(lambda self: self.pages.key_addrs)
+    key_block_strides = property(lambda self: self.pages.key_block_strides)
+    decay_base_addrs = property(lambda self: self.pages.decay_addrs)
+    decay_block_strides = property(lambda self: self.pages.decay_block_strides)
 
     @classmethod
     def from_tensors(
@@ -669,123 +756,21 @@ class GDNRecoverSSMCommitContext:
         max_num_reqs: int,
         conv_dim_first: bool = True,
     ) -> "GDNRecoverSSMCommitContext":
-        """Bind layer-owned page views and allocate reusable commit-plan buffers."""
-        _require(len(checkpoints) > 0, "commit requires at least one layer")
-        _require(len(conv_states) == len(checkpoints) == len(replays), "conv, state and replay lists differ")
-        _require(0 < spec_query_len <= MAX_SPEC_QUERY_LEN, f"spec_query_len must be in [1, {MAX_SPEC_QUERY_LEN}]")
+        """Bind the layers' pages and records (conv states token-major when
+        ``conv_dim_first`` is false) and allocate the plan arrays."""
         if not conv_dim_first:
             conv_states = [s.transpose(-1, -2) for s in conv_states]
-        ref = checkpoints[0]
-        _require(ref.ndim == 4, "checkpoint must be four-dimensional")
-        nb, HV, V, K = ref.shape
-        _dev = ref.device
-        for s in checkpoints:
-            _require(
-                s.shape == ref.shape and s.dtype == ref.dtype and s.stride()[1:] == ref.stride()[1:] and s.device == _dev,
-                "layers need matching checkpoints",
-            )
-        soa = isinstance(replays[0], ReplayRecordBuffers)
-        _require(
-            all(isinstance(r, ReplayRecordBuffers) == soa for r in replays),
-            "packed and typed records cannot share a commit context",
-        )
-        if soa:
-            corrs = [r.correction for r in replays]
-            keys = [r.key for r in replays]
-            decays = [r.decay for r in replays]
-            H = keys[0].shape[1]
-            _require(H > 0 and HV % H == 0, "record key heads are incompatible")
-            for c, k, d in zip(corrs, keys, decays):
-                _require(
-                    c.shape == corrs[0].shape
-                    and tuple(c.shape[1:]) == (HV, spec_query_len, V)
-                    and tuple(k.shape) == (c.shape[0], H, spec_query_len, K)
-                    and tuple(d.shape) == (c.shape[0], HV, spec_query_len)
-                    and c.dtype == d.dtype == torch.float32
-                    and k.dtype in (torch.float16, torch.bfloat16, torch.float32)
-                    and k.dtype == keys[0].dtype
-                    and all(t.device == _dev for t in (c, k, d))
-                    and c.stride()[1:] == corrs[0].stride()[1:]
-                    and k.stride()[1:] == keys[0].stride()[1:]
-                    and d.stride()[1:] == decays[0].stride()[1:],
-                    "layers need matching typed replay geometry/dtypes/strides",
-                )
-        else:
-            corrs = keys = decays = list(replays)
-            H = HV
-            for r in replays:
-                _require(
-                    r.ndim == 4
-                    and tuple(r.shape[1:]) == (HV, spec_query_len, V + K + 1)
-                    and r.shape == replays[0].shape
-                    and r.dtype == torch.float32
-                    and r.stride()[1:] == replays[0].stride()[1:]
-                    and r.device == _dev,
-                    "layers need matching packed FP32 replay buffers",
-                )
-        conv_ref = conv_states[0]
-        _require(
-            conv_ref.ndim == 3 and conv_ref.shape[0] == nb,
-            "conv state must be [blocks, dim, window] with the checkpoint's block count",
-        )
-        for c in conv_states:
-            _require(
-                c.shape == conv_ref.shape and c.dtype == conv_ref.dtype and c.stride()[1:] == conv_ref.stride()[1:] and c.device == _dev,
-                "layers need matching conv states",
-            )
-        conv_dim, conv_len = conv_ref.shape[1:]
-        hist = conv_len - spec_query_len + 1
-        _require(hist > 0, "conv state is shorter than its window")
-        dev = ref.device
-        key_off = 0 if soa else V * 4
-        decay_off = 0 if soa else (V + K) * 4
-
-        def addr(ts, off=0):
-            return _ptr_table(ts, dev, [off] * len(ts) if off else None)
-
-        def bstr(ts):
-            return torch.tensor([t.stride(0) for t in ts], dtype=torch.int64, device=dev)
-
-        def z():
-            return torch.zeros(max_num_reqs, dtype=torch.int32, device=dev)
-
-        context = cls(
-            tuple(conv_states),
-            addr(conv_states),
-            bstr(conv_states),
-            torch.tensor([s.stride(1) for s in conv_states], dtype=torch.int64, device=dev),
-            torch.tensor([s.stride(2) for s in conv_states], dtype=torch.int64, device=dev),
-            hist,
-            tuple(checkpoints),
-            addr(checkpoints),
-            bstr(checkpoints),
-            tuple(replays),
-            addr(corrs),
-            bstr(corrs),
-            z(),
-            z(),
-            z(),
-            z(),
-            spec_query_len,
-            nb,
-        )
-        context.records = list(replays)
-        context.record_rows = int(corrs[0].shape[0])
-        context.record_layout = "soa" if soa else "packed"
-        context.num_key_heads = int(H)
-        context.key_dtype = keys[0].dtype if soa else torch.float32
-        context.correction_base_addrs = context.replay_base_addrs
-        context.correction_block_strides = context.replay_block_strides
-        context.key_base_addrs = addr(keys, key_off)
-        context.key_block_strides = bstr(keys)
-        context.decay_base_addrs = addr(decays, decay_off)
-        context.decay_block_strides = bstr(decays)
-        context.record_bytes = sum(record_nbytes(r) for r in replays)
-        context.align_valid = z()
-        context.align_col = z()
-        context.plan_source = z()  # canonical source page of each planned row (NULL when invalid)
-        context.pending_rows = torch.arange(max_num_reqs, dtype=torch.int32, device=dev)
-        return context
+        typed = [isinstance(r, ReplayRecordBuffers) for r in replays]
+        require(all(typed) or not any(typed), "packed and typed records cannot share a commit context")
+        check_layers(conv_states, checkpoints, replays, window=spec_query_len, typed=bool(typed and typed[0]),
+                     max_window=MAX_SPEC_QUERY_LEN)
+        pages = LayerPages(conv_states, checkpoints, replays, checkpoints[0].device)
+        first = pages.first_planes
+        return cls(pages, spec_query_len=spec_query_len, max_num_reqs=max_num_reqs,
+                   conv_history_len=conv_states[0].shape[2] - spec_query_len + 1,
+                   record_layout="packed" if first.packed else "soa",
+                   num_key_heads=checkpoints[0].shape[1] if first.packed else first.key.shape[1],
+                   key_dtype=torch.float32 if first.packed else first.key.dtype)
 
     @classmethod
     def create(
@@ -799,11 +784,11 @@ class GDNRecoverSSMCommitContext:
         key_dtype: torch.dtype | None = None,
         conv_dim_first: bool | None = None,
     ) -> "GDNRecoverSSMCommitContext":
-        """Build the context from live layers' ``kv_cache`` pages (conv, checkpoint).
-
-        Records are allocated here as row-indexed scratch and handed to each
-        layer as ``layer._gdn_recoverssm_records``.
-        """
+        """The context of live layers whose ``kv_cache`` is (conv state,
+        checkpoint). Records are row-indexed step scratch, not cache pages:
+        they are allocated here, ``record_rows`` (default ``max_num_reqs``)
+        rows per layer, and handed to each layer as
+        ``layer._gdn_recoverssm_records`` for its verify to write."""
         if conv_dim_first is None:
             try:  # vLLM decides the conv layout when it is installed
                 from vllm.model_executor.layers.mamba.mamba_utils import is_conv_state_dim_first
@@ -813,29 +798,23 @@ class GDNRecoverSSMCommitContext:
                 conv_dim_first = True
         if any(len(layer.kv_cache) != 2 for layer in layers):
             raise ValueError("GDN RecoverSSM expects conv and checkpoint pages; the replay records live outside the cache")
-        state0 = layers[0].kv_cache[1]
-        num_heads, head_v, head_k = state0.shape[1], state0.shape[2], state0.shape[3]
-        rows = int(record_rows or max_num_reqs)
-        key_heads = num_heads if num_key_heads is None else int(num_key_heads)
-        record_key_dtype = torch.float32 if key_dtype is None else key_dtype
+        pages0 = layers[0].kv_cache[1]
+        _, HV, V, K = pages0.shape
         records = [
-            ReplayRecordBuffers.allocate(
-                rows, num_heads, key_heads, spec_query_len, head_v, head_k, device=state0.device, key_dtype=record_key_dtype
-            )
+            ReplayRecordBuffers.allocate(int(record_rows or max_num_reqs), HV,
+                                         HV if num_key_heads is None else int(num_key_heads), spec_query_len, V, K,
+                                         device=pages0.device, key_dtype=key_dtype or torch.float32)
             for _ in layers
         ]
-        context = cls.from_tensors(
-            [layer.kv_cache[0] for layer in layers],
-            [layer.kv_cache[1] for layer in layers],
-            records,
-            spec_query_len=spec_query_len,
-            max_num_reqs=max_num_reqs,
-            conv_dim_first=conv_dim_first,
-        )
-        context.records = records
+        context = cls.from_tensors([layer.kv_cache[0] for layer in layers], [layer.kv_cache[1] for layer in layers],
+                                   records, spec_query_len=spec_query_len, max_num_reqs=max_num_reqs,
+                                   conv_dim_first=conv_dim_first)
         for layer, record in zip(layers, records):
             layer._gdn_recoverssm_records = record
         return context
+
+    # -- preparation (nothing is compiled at run time: these only check that
+    # -- every serving signature is accepted and its entry point is there) --
 
     def make_commit_specs(
         self,
@@ -848,62 +827,46 @@ class GDNRecoverSSMCommitContext:
         mamba_block_size=None,
         commit_conv: bool = True,
     ) -> tuple:
-        """Build the launch specs for one step, without launching them."""
+        """The launch specs of one step's commit, not launched."""
         specs: list = []
-        self.commit(
-            num_accepted_tokens,
-            state_indices,
-            query_start_loc,
-            request_indices=request_indices,
-            block_table=block_table,
-            num_computed_tokens=num_computed_tokens,
-            mamba_block_size=mamba_block_size,
-            commit_conv=commit_conv,
-            _collect=specs,
-        )
+        self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices=request_indices,
+                    block_table=block_table, num_computed_tokens=num_computed_tokens,
+                    mamba_block_size=mamba_block_size, commit_conv=commit_conv, _collect=specs)
         return tuple(specs)
 
     def prepare_verify(self, *, activation_dtype, state_table_width: int | None = None, device=None) -> list:
-        """Validate the serving verify signatures (contiguous and combined-QKV
-        value views, activation-typed and FP32 beta) without touching state."""
+        """Check the serving verify signatures of this epoch without touching
+        a page: a contiguous and a combined-QKV value view (the fused
+        projection's token stride), each with an FP32 and an activation-typed
+        beta; one report dict per signature."""
         device = self.checkpoints[0].device if device is None else device
-        record = self.records[0]
-        _, hv, value_dim, key_dim = self.checkpoints[0].shape
-        key_heads = self.num_key_heads
-        window = self.spec_query_len
-        width = int(state_table_width or window)
-        _require(width > 0, "verify preparation requires a positive table stride")
-        q = torch.empty((1, window, key_heads, key_dim), dtype=activation_dtype, device=device)
-        k = torch.empty_like(q)
-        g = torch.empty((1, window, hv), dtype=torch.float32, device=device)
-        output = torch.empty((1, window, hv, value_dim), dtype=activation_dtype, device=device)
-        state_table = torch.empty((1, width), dtype=torch.int32, device=device)
-        offsets = torch.empty(2, dtype=torch.int32, device=device)
+        _, HV, V, K = self.checkpoints[0].shape
+        H, Q = self.num_key_heads, self.spec_query_len
+        width = int(state_table_width or Q)
+        require(width > 0, "verify preparation requires a positive table stride")
+
+        def blank(*shape, dtype=activation_dtype):
+            return torch.empty(shape, dtype=dtype, device=device)
+
+        q, k = blank(1, Q, H, K), blank(1, Q, H, K)
+        g, out = blank(1, Q, HV, dtype=torch.float32), blank(1, Q, HV, V)
+        table, offsets = blank(1, width, dtype=torch.int32), blank(2, dtype=torch.int32)
+        fused = blank(1, Q, 2 * H * K + HV * V)
+        value_views = {False: blank(1, Q, HV, V), True: fused[:, :, 2 * H * K:].view(1, Q, HV, V)}
         report = []
-        for packed_value in (False, True):
-            if packed_value:
-                features = 2 * key_heads * key_dim + hv * value_dim
-                combined = torch.empty((1, window, features), dtype=activation_dtype, device=device)
-                value = combined[:, :, 2 * key_heads * key_dim :].view(1, window, hv, value_dim)
-            else:
-                value = torch.empty_like(output)
-            for beta_dtype in tuple(dict.fromkeys((torch.float32, activation_dtype))):
-                beta = torch.empty((1, window, hv), dtype=beta_dtype, device=device)
+        for combined, value in value_views.items():
+            for beta_dtype in dict.fromkeys((torch.float32, activation_dtype)):
                 specs: list = []
-                gdn_recoverssm_verify(
-                    g, beta, q, k, value, checkpoint_state=self.checkpoints[0], replay_cache=record,
-                    query_start_loc=offsets, state_indices=state_table[:, 0], spec_query_len=window,
-                    qk_already_normalized=True, out=output, _collect=specs,
-                )
+                gdn_recoverssm_verify(g, blank(1, Q, HV, dtype=beta_dtype), q, k, value,
+                                      checkpoint_state=self.checkpoints[0], replay_cache=self.records[0],
+                                      query_start_loc=offsets, state_indices=table[:, 0], spec_query_len=Q,
+                                      qk_already_normalized=True, out=out, _collect=specs)
                 for spec in specs:
                     spec.compile_only()
-                report.append(
-                    dict(
-                        activation_dtype=str(activation_dtype), beta_dtype=str(beta_dtype),
-                        value_token_stride=value.stride(1), state_index_stride=width, state_blocks=self.num_blocks,
-                        record_rows=self.record_rows, num_value_heads=hv, num_key_heads=key_heads, window=window,
-                    )
-                )
+                report.append(dict(activation_dtype=str(activation_dtype), beta_dtype=str(beta_dtype),
+                                   value_token_stride=value.stride(1), state_index_stride=width,
+                                   state_blocks=self.num_blocks, record_rows=self.record_rows, num_value_heads=HV,
+                                   num_key_heads=H, window=Q))
         self.verify_prepare_report = tuple(report)
         return report
 
@@ -923,29 +886,44 @@ class GDNRecoverSSMCommitContext:
         query_index_dtype=torch.int32,
         computed_dtype=torch.int32,
     ) -> list[int]:
-        """Validate the none/align commit signatures for every row count."""
-        _require(
-            not align_mode or (mamba_block_size is not None and mamba_block_size >= self.spec_query_len),
-            "align preparation requires the runtime block size",
-        )
-        compiled_rows = []
+        """Check the none / align commit signature for every batch size up to
+        ``capacity`` (and the record rows); returns the row counts checked."""
+        require(not align_mode or (mamba_block_size is not None and mamba_block_size >= self.spec_query_len),
+                "align preparation requires the runtime block size")
+        width = int(block_table_width or state_table_width)
+        checked = []
         for rows in range(1, min(capacity, self.record_rows) + 1):
-            table = torch.empty((rows, state_table_width), dtype=state_index_dtype, device=device)
-            qsl = torch.empty(rows + 1, dtype=query_index_dtype, device=device)
-            accepted = torch.empty(rows, dtype=accepted_dtype, device=device)
-            mapping = torch.empty(rows, dtype=request_index_dtype, device=device) if request_mapping else None
-            bt = computed = None
-            if align_mode:
-                width = int(block_table_width or state_table_width)
-                bt = torch.empty((rows, width), dtype=state_index_dtype, device=device)
-                computed = torch.empty(rows, dtype=computed_dtype, device=device)
-            for spec in self.make_commit_specs(
-                accepted, table[:, 0], qsl, request_indices=mapping, block_table=bt, num_computed_tokens=computed,
-                mamba_block_size=mamba_block_size if align_mode else None,
-            ):
+            def blank(*shape, dtype):
+                return torch.empty(shape, dtype=dtype, device=device)
+
+            align = dict(block_table=blank(rows, width, dtype=state_index_dtype),
+                         num_computed_tokens=blank(rows, dtype=computed_dtype),
+                         mamba_block_size=mamba_block_size) if align_mode else {}
+            specs = self.make_commit_specs(
+                blank(rows, dtype=accepted_dtype), blank(rows, state_table_width, dtype=state_index_dtype)[:, 0],
+                blank(rows + 1, dtype=query_index_dtype),
+                request_indices=blank(rows, dtype=request_index_dtype) if request_mapping else None, **align)
+            for spec in specs:
                 spec.compile_only()
-            compiled_rows.append(rows)
-        return compiled_rows
+            checked.append(rows)
+        return checked
+
+    # -- the commit --
+
+    def _plan_spec(self, accepted, state_indices, qsl, request_indices, block_table, num_computed, block_size,
+                   rows) -> _LaunchSpec:
+        groups = N.PlanGroups()
+        _fill_plan_group(groups[0], state_indices=state_indices, query_start_loc=qsl, request_indices=request_indices,
+                         block_table=block_table, num_computed_tokens=num_computed, block_size=block_size,
+                         num_blocks=self.num_blocks)
+        align = block_table is not None
+        args = (accepted.data_ptr(), N.dtype_code(accepted.dtype), accepted.stride(0), accepted.shape[0], groups, 1,
+                self.plan_source.data_ptr(), self.commit_lens.data_ptr(), self.final_state_indices.data_ptr(),
+                self.boundary_state_indices.data_ptr(), self.boundary_recovery_lens.data_ptr(),
+                self.align_valid.data_ptr(), self.align_col.data_ptr(), None, N.DT_I32, 0, None, None, 0, rows,
+                self.commit_lens.shape[0], NULL_BLOCK_ID, self.spec_query_len, N.PLAN_ALIGN if align else 0)
+        keep = (groups, accepted, state_indices, qsl, request_indices, block_table, num_computed)
+        return _LaunchSpec("plan", _lib().gdn_recoverssm_plan, args, state_indices.device, keepalive=keep)
 
     def commit(
         self,
@@ -960,159 +938,36 @@ class GDNRecoverSSMCommitContext:
         _collect: list | None = None,
         _fold_source: torch.Tensor | None = None,
     ) -> None:
-        """Fold accepted GDN and convolution inputs into every layer's checkpoint."""
-        batch = state_indices.shape[0]
-        if batch == 0:
+        """Fold every committed row's accepted prefix into its final page (and
+        its boundary snapshot in align mode) in every layer, then compact the
+        conv states. ``_fold_source`` (internal) keeps the plan and the fold
+        apart, the fold reading its source pages from that array."""
+        rows = state_indices.shape[0]
+        if rows == 0:
             return
-        _require(state_indices.ndim == 1, "state indices must be one-dimensional")
-        _require(batch <= self.commit_lens.shape[0], "commit batch exceeds its plan capacity")
-        _require(query_start_loc.ndim == 1 and query_start_loc.shape[0] == batch + 1, "commit metadata is incompatible")
-        _require(request_indices is None or request_indices.shape[0] >= batch, "request mapping is too short")
-        _require(
-            num_accepted_tokens.ndim == 1 and (request_indices is not None or num_accepted_tokens.shape[0] >= batch),
-            "accepted-token counts are too short",
-        )
-        _align = (block_table, num_computed_tokens, mamba_block_size)
-        _require(all(x is None for x in _align) or all(x is not None for x in _align), "align metadata is incomplete")
-        _require(
-            mamba_block_size is None or mamba_block_size >= self.spec_query_len,
-            "align block size must cover one speculative window",
-        )
-        _require(
-            block_table is None or (block_table.ndim == 2 and block_table.shape[1] > 0),
-            "block table must be two-dimensional with a positive width",
-        )
-        _dev = self.checkpoints[0].device
-        _require(
-            all(
-                t_ is None or t_.device == _dev
-                for t_ in (num_accepted_tokens, state_indices, query_start_loc, request_indices, block_table, num_computed_tokens)
-            ),
-            "commit inputs must be on the same device",
-        )
-        _require(_dev.type == "cuda", "the commit runs on a HIP device")
+        enforce(_commit_rules(self, num_accepted_tokens, state_indices, query_start_loc, request_indices,
+                              block_table, num_computed_tokens, mamba_block_size))
         align = block_table is not None
-        lib = _lib()
-        grp = N.PlanGroups()
-        gr = grp[0]
-        gr.state_indices = state_indices.data_ptr()
-        gr.si_stride = state_indices.stride(0)
-        gr.si_dtype = N.dtype_code(state_indices.dtype)
-        gr.query_start_loc = query_start_loc.data_ptr()
-        gr.qsl_stride = query_start_loc.stride(0)
-        gr.qsl_dtype = N.dtype_code(query_start_loc.dtype)
-        if request_indices is not None:
-            gr.request_indices = request_indices.data_ptr()
-            gr.map_stride = request_indices.stride(0)
-            gr.map_dtype = N.dtype_code(request_indices.dtype)
-        if align:
-            gr.block_table = block_table.data_ptr()
-            gr.table_row_stride = block_table.stride(0)
-            gr.table_col_stride = block_table.stride(1)
-            gr.table_width = block_table.shape[1]
-            gr.table_rows = block_table.shape[0]
-            gr.table_dtype = N.dtype_code(block_table.dtype)
-            gr.num_computed = num_computed_tokens.data_ptr()
-            gr.computed_stride = num_computed_tokens.stride(0)
-            gr.computed_len = num_computed_tokens.shape[0]
-            gr.computed_dtype = N.dtype_code(num_computed_tokens.dtype)
-            gr.block_size = int(mamba_block_size)
-        else:
-            gr.block_size = 1
-            gr.table_width = 1
-        gr.num_blocks = self.num_blocks
-        plan_args = (
-            num_accepted_tokens.data_ptr(),
-            N.dtype_code(num_accepted_tokens.dtype),
-            num_accepted_tokens.stride(0),
-            num_accepted_tokens.shape[0],
-            grp,
-            1,
-            self.plan_source.data_ptr(),
-            self.commit_lens.data_ptr(),
-            self.final_state_indices.data_ptr(),
-            self.boundary_state_indices.data_ptr(),
-            self.boundary_recovery_lens.data_ptr(),
-            self.align_valid.data_ptr(),
-            self.align_col.data_ptr(),
-            None,
-            N.DT_I32,
-            0,
-            None,
-            None,
-            0,
-            batch,
-            self.commit_lens.shape[0],
-            NULL_BLOCK_ID,
-            self.spec_query_len,
-            N.PLAN_ALIGN if align else 0,
-        )
-        keep = (num_accepted_tokens, state_indices, query_start_loc, request_indices, block_table, num_computed_tokens)
-        plan_spec = _LaunchSpec("plan", lib.gdn_recoverssm_plan, plan_args, _dev, keepalive=(grp,) + keep)
-        specs = [plan_spec]
-        num_layers = len(self.checkpoints)
+        device = self.checkpoints[0].device
+        plan = self._plan_spec(num_accepted_tokens, state_indices, query_start_loc, request_indices, block_table,
+                               num_computed_tokens, mamba_block_size, rows)
+        arrays = (self.commit_lens, self.final_state_indices, self.boundary_state_indices, self.boundary_recovery_lens)
+        conv = None
         if commit_conv:
-            conv_ref = self.conv_states[0]
-            conv_args = (
-                self.conv_state_base_addrs.data_ptr(),
-                self.conv_state_block_strides.data_ptr(),
-                self.conv_state_dim_strides.data_ptr(),
-                self.conv_state_token_strides.data_ptr(),
-                state_indices.data_ptr(),
-                N.dtype_code(state_indices.dtype),
-                state_indices.stride(0),
-                self.commit_lens.data_ptr(),
-                self.final_state_indices.data_ptr(),
-                self.boundary_state_indices.data_ptr(),
-                self.boundary_recovery_lens.data_ptr(),
-                None,
-                self.commit_lens.shape[0],
-                NULL_BLOCK_ID,
-                batch,
-                num_layers,
-                conv_ref.shape[1],
-                self.conv_history_len,
-                conv_ref.shape[2],
-                self.num_blocks,
-                conv_ref.element_size(),
-                1 if align else 0,
-            )
-            _require(conv_ref.element_size() in (2, 4), "conv state elements must be 2 or 4 bytes")
-            specs.append(_LaunchSpec("conv", lib.gdn_recoverssm_conv_compact, conv_args, _dev, keepalive=keep))
-        ref = self.checkpoints[0]
-        _, HV, V, K = ref.shape
-        record = self.replays[0]
-        rr, kr, dr, _, _ = _record_planes(record, V, K)
-        soa = self.record_layout == "soa"
-        key_strides = kr.stride()[1:3] if soa else rr.stride()[1:3]
-        decay_strides = dr.stride()[1:3] if soa else rr.stride()[1:3]
-        fold_spec = _make_fold_spec(
-            ref=ref,
-            record_rows=rr.shape[0],
-            corr_strides=rr.stride()[1:3],
-            key_strides=key_strides,
-            decay_strides=decay_strides,
-            key_heads=self.num_key_heads,
-            key_dtype=self.key_dtype,
-            num_layers=num_layers,
-            rows=batch,
-            plan_capacity=self.commit_lens.shape[0],
-            num_blocks=self.num_blocks,
-            spec_query_len=self.spec_query_len,
-            tables=(
-                self.state_base_addrs, self.state_block_strides, self.correction_base_addrs, self.correction_block_strides,
-                self.key_base_addrs, self.key_block_strides, self.decay_base_addrs, self.decay_block_strides,
-            ),
-            layer_groups=None,
-            source=state_indices if _fold_source is None else _fold_source,
-            plan=(self.commit_lens, self.final_state_indices, self.boundary_state_indices, self.boundary_recovery_lens),
-            refs=(rr, kr, dr),
-        )
-        specs.append(fold_spec)
+            conv = _conv_spec(self.pages, source=state_indices, source_dtype=N.dtype_code(state_indices.dtype),
+                              source_stride=state_indices.stride(0), plan=arrays, layer_groups=None,
+                              capacity=self.commit_lens.shape[0], rows=rows, history=self.conv_history_len,
+                              max_blocks=self.num_blocks, align=align, device=device,
+                              keep=(state_indices, query_start_loc))
+        fold = _make_fold_spec(pages=self.pages, record_rows=self.record_rows, key_heads=self.num_key_heads,
+                               key_dtype=self.key_dtype, rows=rows, plan_capacity=self.commit_lens.shape[0],
+                               num_blocks=self.num_blocks, spec_query_len=self.spec_query_len, layer_groups=None,
+                               source=state_indices if _fold_source is None else _fold_source, plan=arrays)
         if _fold_source is None:
-            # One launch plans and folds; the conv compaction, which reads the
-            # stored plan, follows it.
-            specs = [_fuse_plan_fold(plan_spec, fold_spec)] + specs[1:-1]
+            # One launch plans and folds; the conv compaction reads the plan it stores.
+            specs = [_fuse_plan_fold(plan, fold)] + ([conv] if conv else [])
+        else:
+            specs = [plan] + ([conv] if conv else []) + [fold]
         if _collect is not None:
             _collect.extend(specs)
         else:
@@ -1132,11 +987,11 @@ class GDNRecoverSSMCommitContext:
         commit_conv: bool = True,
         _collect: list | None = None,
     ) -> tuple:
-        """Plan the commit (and compact the conv states) but leave the fold to
-        the next step's ``gdn_recoverssm_verify_deferred``; returns one
-        ``PendingCommit`` per layer. ``flush_deferred`` applies the pending
-        fold directly instead (for a step that runs no verify)."""
-        _require(self.record_layout == "soa", "the deferred commit needs typed record buffers")
+        """Plan the commit and compact the conv states now, and leave the fold
+        to the next step's ``gdn_recoverssm_verify_deferred``: returns one
+        ``PendingCommit`` per layer. ``flush_deferred`` folds instead (the
+        last step, or rows whose requests left)."""
+        require(self.record_layout == "soa", "the deferred commit needs typed record buffers")
         specs: list = []
         self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices=request_indices,
                     block_table=block_table, num_computed_tokens=num_computed_tokens,
@@ -1150,12 +1005,10 @@ class GDNRecoverSSMCommitContext:
         else:
             for sp in now:
                 sp.launch()
-        return tuple(
-            PendingCommit(self.pending_rows, self.plan_source, self.commit_lens, self.final_state_indices,
-                          self.boundary_state_indices, self.boundary_recovery_lens, rec,
-                          num_rows=self._deferred_rows)
-            for rec in self.records
-        )
+        plan = (self.plan_source, self.commit_lens, self.final_state_indices, self.boundary_state_indices,
+                self.boundary_recovery_lens)
+        return tuple(PendingCommit(self.pending_rows, *plan, rec, num_rows=self._deferred_rows)
+                     for rec in self.records)
 
     def flush_deferred(self, rows: Sequence[int] | torch.Tensor | None = None, _collect: list | None = None) -> None:
         """Apply the last ``commit_deferred`` plan with the ordinary fold.
@@ -1167,13 +1020,11 @@ class GDNRecoverSSMCommitContext:
         flush or by the verify that continues it, never both.
         """
         spec = getattr(self, "_deferred_fold", None)
-        _require(spec is not None, "no deferred commit to flush")
+        require(spec is not None, "no deferred commit to flush")
         if rows is not None:
             pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
-            _require(
-                bool(((pick >= 0) & (pick < self._deferred_rows)).all()),
-                "flushed rows must be rows of the pending plan",
-            )
+            require(bool(((pick >= 0) & (pick < self._deferred_rows)).all()),
+                    "flushed rows must be rows of the pending plan")
             if pick.numel() == 0:
                 return
             # The same fold over a length array that keeps only the picked rows.
@@ -1181,7 +1032,7 @@ class GDNRecoverSSMCommitContext:
             idx = pick.to(lengths.device)
             lengths[idx] = self.commit_lens[idx]
             args = list(spec.args)
-            args[14] = lengths.data_ptr()  # fold arguments: ..., source, lengths, finals, ...
+            args[_FOLD_LENGTHS_ARG] = lengths.data_ptr()
             spec = _LaunchSpec(spec.name, spec.fn, tuple(args), spec.device, keepalive=spec.keepalive + (lengths,))
         if _collect is not None:
             _collect.append(spec)
@@ -1189,114 +1040,14 @@ class GDNRecoverSSMCommitContext:
             spec.launch()
 
 
-def _fuse_plan_fold(plan: _LaunchSpec, fold: _LaunchSpec) -> _LaunchSpec:
-    """``gdn_recoverssm_plan_fold``: the plan launch and the fold launch that
-    reads its arrays, as one launch with identical results (every fold
-    workgroup plans its own row; extra workgroups store the plan arrays)."""
-    launch = N.plan_launch(plan.args)
-    # fold arguments: 4 reference tensors, 8 tables, layer_groups, source,
-    # 4 plan arrays, config, config length, extension
-    args = (ctypes.byref(launch),) + tuple(fold.args[:13]) + tuple(fold.args[18:])
-    spec = _LaunchSpec(
-        "plan_fold", _lib().gdn_recoverssm_plan_fold, args, fold.device, keepalive=(plan.keepalive, fold.keepalive, launch)
-    )
-    spec.config = fold.config
-    return spec
-
-
-def _make_fold_spec(
-    *,
-    ref,
-    record_rows,
-    corr_strides,
-    key_strides,
-    decay_strides,
-    key_heads,
-    key_dtype,
-    num_layers,
-    rows,
-    plan_capacity,
-    num_blocks,
-    spec_query_len,
-    tables,
-    layer_groups,
-    source,
-    plan,
-    refs,
-) -> _LaunchSpec:
-    """Fold launch shared by the single-context and grouped commits."""
-    _, HV, V, K = ref.shape
-    es = ref.element_size()
-    chunk = 16 // es
-    _require(ref.dtype in (torch.float32, torch.bfloat16, torch.float16), "checkpoint dtype is not supported")
-    _require(key_dtype in (torch.float32, torch.bfloat16, torch.float16), "record key dtype is not supported")
-    _require(
-        K <= MAX_KEY_DIM and K % chunk == 0 and ref.stride(3) == 1 and all(s_ % chunk == 0 for s_ in ref.stride()[:3]) and V <= 1024,
-        f"checkpoint rows must be contiguous, 16-byte aligned, K <= {MAX_KEY_DIM} a multiple of {chunk}, V <= 1024",
-    )
-    config = (
-        rows,
-        num_layers,
-        HV,
-        key_heads,
-        spec_query_len,
-        num_blocks,
-        record_rows,
-        plan_capacity,
-        NULL_BLOCK_ID,
-        ref.stride(1),
-        ref.stride(2),
-        corr_strides[0],
-        corr_strides[1],
-        key_strides[0],
-        key_strides[1],
-        decay_strides[0],
-        decay_strides[1],
-    )
-    ext = N.FoldExt(
-        key_dim=K,
-        value_dim=V,
-        state_dtype=N.dtype_code(ref.dtype),
-        key_dtype=N.dtype_code(key_dtype),
-        source_dtype=N.dtype_code(source.dtype),
-        reserved=0,
-        source_stride=source.stride(0),
-        state_k_stride=ref.stride(3),
-    )
-    cfg = N.i64_array(config)
-    lengths, finals, boundaries, boundary_lens = plan
-    rr, kr, dr = refs
-    args = (
-        ref.data_ptr(),
-        rr.data_ptr(),
-        kr.data_ptr(),
-        dr.data_ptr(),
-        *(t.data_ptr() for t in tables),
-        None if layer_groups is None else layer_groups.data_ptr(),
-        source.data_ptr(),
-        lengths.data_ptr(),
-        finals.data_ptr(),
-        boundaries.data_ptr(),
-        boundary_lens.data_ptr(),
-        cfg,
-        N.FOLD_CONFIG_FIELDS,
-        ctypes.byref(ext),
-    )
-    spec = _LaunchSpec(
-        "fold",
-        _lib().gdn_recoverssm_fold,
-        args,
-        ref.device,
-        keepalive=(ref, rr, kr, dr, *tables, layer_groups, source, *plan, cfg, ext),
-    )
-    spec.config = tuple(int(x) for x in config)
-    return spec
-
-
 __all__ = [
     "GDNRecoverSSMCommitContext",
+    "PendingCommit",
     "ReplayRecordBuffers",
+    "continue_pending",
     "gdn_recoverssm_verify",
+    "gdn_recoverssm_verify_deferred",
+    "gdn_recoverssm_verify_gated",
     "record_geometry_bytes",
     "record_nbytes",
 ]
