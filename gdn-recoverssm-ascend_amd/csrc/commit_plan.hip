@@ -52,14 +52,18 @@ __global__ __launch_bounds__(256) void conv_compact_kernel(
     const int64_t *__restrict__ dim_strides, const int64_t *__restrict__ token_strides, const void *source,
     int32_t source_dtype, int64_t source_stride, const int32_t *__restrict__ lengths,
     const int32_t *__restrict__ finals, const int32_t *__restrict__ boundaries,
-    const int32_t *__restrict__ boundary_lens, const int32_t *__restrict__ layer_groups, int64_t cap,
+    const int32_t *__restrict__ boundary_lens, const int32_t *__restrict__ layer_groups, int64_t groups, int64_t cap,
     int64_t null_block, int64_t rows, int64_t conv_dim, int64_t history, int64_t window, int64_t num_blocks,
     int32_t align, int64_t dim_tiles) {
   const int64_t wg = blockIdx.x;
   const int64_t tile = wg % dim_tiles;
   const int64_t row = (wg / dim_tiles) % rows;
   const int64_t layer = wg / (dim_tiles * rows);
-  const int64_t plan_row = (layer_groups ? int64_t(layer_groups[layer]) * cap : 0) + row;
+  // A layer mapped outside the plan's groups compacts nothing (as the fold
+  // folds nothing for it).
+  const int64_t group = layer_groups ? int64_t(layer_groups[layer]) : 0;
+  if (group < 0 || group >= groups) return;
+  const int64_t plan_row = group * cap + row;
   const int64_t src = load_index(source, plan_row * source_stride, source_dtype);
   const int64_t n = lengths[plan_row];
   const int64_t fin = finals[plan_row];
@@ -285,15 +289,15 @@ extern "C" int gdn_recoverssm_plan(const void *sampled, int32_t sampled_dtype, i
   return GDN_OK;
 }
 
-extern "C" int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int64_t *conv_block_strides,
-                                           const int64_t *conv_dim_strides, const int64_t *conv_token_strides,
-                                           const void *source, int32_t source_dtype, int64_t source_stride,
-                                           const int32_t *lengths, const int32_t *final_indices,
-                                           const int32_t *boundary_indices, const int32_t *boundary_lengths,
-                                           const int32_t *layer_groups, int64_t plan_capacity,
-                                           int64_t null_block, int64_t num_rows, int64_t num_layers,
-                                           int64_t conv_dim, int64_t history, int64_t window, int64_t num_blocks,
-                                           int32_t element_bytes, int32_t align, void *stream) {
+namespace gdn {
+
+int conv_compact_launch(const int64_t *conv_addrs, const int64_t *conv_block_strides, const int64_t *conv_dim_strides,
+                        const int64_t *conv_token_strides, const void *source, int32_t source_dtype,
+                        int64_t source_stride, const int32_t *lengths, const int32_t *final_indices,
+                        const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                        const int32_t *layer_groups, int64_t plan_groups, int64_t plan_capacity, int64_t null_block,
+                        int64_t num_rows, int64_t num_layers, int64_t conv_dim, int64_t history, int64_t window,
+                        int64_t num_blocks, int32_t element_bytes, int32_t align, bool check_only, void *stream) {
   if (!conv_addrs || !conv_block_strides || !conv_dim_strides || !conv_token_strides || !source || !lengths ||
       !final_indices || !boundary_indices || !boundary_lengths || !index_dtype_ok(source_dtype)) {
     set_error("conv_compact: missing table or plan pointer");
@@ -316,14 +320,15 @@ extern "C" int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int6
     set_error("conv_compact: grid too large");
     return GDN_ERR_UNSUPPORTED;
   }
+  if (check_only) return GDN_OK;
   auto s = static_cast<hipStream_t>(stream);
   // Dwords per channel window when it fits the 128-bit fast path, else 0.
   const int64_t wbytes = window * element_bytes;
   const int wdw = (wbytes % 4 == 0 && wbytes <= 16) ? int(wbytes / 4) : 0;
 #define GDN_CONV_ARGS                                                                                          \
   conv_addrs, conv_block_strides, conv_dim_strides, conv_token_strides, source, source_dtype, source_stride, \
-      lengths, final_indices, boundary_indices, boundary_lengths, layer_groups, plan_capacity, null_block,    \
-      num_rows, conv_dim, history, window, num_blocks, align, tiles
+      lengths, final_indices, boundary_indices, boundary_lengths, layer_groups, plan_groups, plan_capacity,   \
+      null_block, num_rows, conv_dim, history, window, num_blocks, align, tiles
 #define GDN_CONV_LAUNCH(E)                                                                                  \
   switch (wdw) {                                                                                            \
     case 1: hipLaunchKernelGGL((conv_compact_kernel<E, 1>), dim3(unsigned(grid)), dim3(256), 0, s, GDN_CONV_ARGS); break; \
@@ -345,6 +350,24 @@ extern "C" int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int6
     return GDN_ERR_LAUNCH;
   }
   return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" int gdn_recoverssm_conv_compact(const int64_t *conv_addrs, const int64_t *conv_block_strides,
+                                           const int64_t *conv_dim_strides, const int64_t *conv_token_strides,
+                                           const void *source, int32_t source_dtype, int64_t source_stride,
+                                           const int32_t *lengths, const int32_t *final_indices,
+                                           const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                                           const int32_t *layer_groups, int64_t plan_capacity,
+                                           int64_t null_block, int64_t num_rows, int64_t num_layers,
+                                           int64_t conv_dim, int64_t history, int64_t window, int64_t num_blocks,
+                                           int32_t element_bytes, int32_t align, void *stream) {
+  // The caller's plan arrays bound the groups a layer may name.
+  return conv_compact_launch(conv_addrs, conv_block_strides, conv_dim_strides, conv_token_strides, source,
+                             source_dtype, source_stride, lengths, final_indices, boundary_indices, boundary_lengths,
+                             layer_groups, INT64_MAX, plan_capacity, null_block, num_rows, num_layers, conv_dim,
+                             history, window, num_blocks, element_bytes, align, false, stream);
 }
 
 extern "C" int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_buckets, const void *request_indices,

@@ -140,4 +140,15 @@ __device__ __forceinline__ void plan_write_row(const PlanArgs &a, int64_t row) {
 // in commit_plan.hip). Returns a GDN_* status with the error message set.
 int make_plan_args(const gdn_plan_launch *launch, PlanArgs *out);
 
+// Host side: checks and launches the conv compaction (commit_plan.hip). A
+// layer whose group lies outside [0, plan_groups) compacts nothing;
+// check_only validates the arguments without launching.
+int conv_compact_launch(const int64_t *conv_addrs, const int64_t *conv_block_strides, const int64_t *conv_dim_strides,
+                        const int64_t *conv_token_strides, const void *source, int32_t source_dtype,
+                        int64_t source_stride, const int32_t *lengths, const int32_t *final_indices,
+                        const int32_t *boundary_indices, const int32_t *boundary_lengths,
+                        const int32_t *layer_groups, int64_t plan_groups, int64_t plan_capacity, int64_t null_block,
+                        int64_t num_rows, int64_t num_layers, int64_t conv_dim, int64_t history, int64_t window,
+                        int64_t num_blocks, int32_t element_bytes, int32_t align, bool check_only, void *stream);
+
 }  // namespace gdn

@@ -125,6 +125,16 @@ class PlanLaunch(ctypes.Structure):  # gdn_plan_launch: gdn_recoverssm_plan's ar
     ]
 
 
+class ConvLaunch(ctypes.Structure):  # gdn_conv_launch: the conv tables of gdn_recoverssm_commit_noalloc
+    _fields_ = [
+        ("conv_addrs", c_vp), ("conv_block_strides", c_vp), ("conv_dim_strides", c_vp), ("conv_token_strides", c_vp),
+        ("conv_dim", c_i64), ("history", c_i64), ("window", c_i64), ("element_bytes", c_i32), ("reserved", c_i32),
+    ]
+
+
+NOALLOC_PLAN_ENTRIES = 32768  # GDN_NOALLOC_PLAN_ENTRIES
+
+
 def plan_launch(plan_args: tuple) -> PlanLaunch:
     """The gdn_recoverssm_plan argument tuple (without the stream) as a PlanLaunch."""
     (sampled, sampled_dtype, sampled_stride, sampled_len, groups, num_groups, source, lens, final, boundary,
@@ -183,6 +193,10 @@ def load() -> ctypes.CDLL:
         lib.gdn_recoverssm_plan_fold.argtypes = [ctypes.POINTER(PlanLaunch)] + [c_vp] * 13 + [
             P_i64, c_i64, ctypes.POINTER(FoldExt), c_vp,
         ]
+        lib.gdn_recoverssm_commit_noalloc.restype = ctypes.c_int
+        lib.gdn_recoverssm_commit_noalloc.argtypes = [ctypes.POINTER(PlanLaunch)] + [c_vp] * 13 + [
+            P_i64, c_i64, ctypes.POINTER(FoldExt), ctypes.POINTER(ConvLaunch), c_vp,
+        ]
         lib.gdn_recoverssm_plan.restype = ctypes.c_int
         lib.gdn_recoverssm_plan.argtypes = [
             c_vp, c_i32, c_i64, c_i64,  # sampled
@@ -219,6 +233,7 @@ def exported_symbols() -> tuple[str, ...]:
         "gdn_recoverssm_verify_deferred",
         "gdn_recoverssm_fold",
         "gdn_recoverssm_plan_fold",
+        "gdn_recoverssm_commit_noalloc",
         "gdn_recoverssm_plan",
         "gdn_recoverssm_conv_compact",
         "gdn_recoverssm_publish",

@@ -265,6 +265,50 @@ int gdn_recoverssm_plan_fold(const gdn_plan_launch *plan, void *state_ref, const
                              const int64_t *decay_block_strides, const int32_t *layer_groups,
                              const int64_t *config, int64_t config_len, const gdn_fold_ext *ext, void *stream);
 
+/* Conv-state tables of one commit, for gdn_recoverssm_commit_noalloc: the
+ * per-layer DEVICE tables and sizes of gdn_recoverssm_conv_compact below. */
+typedef struct gdn_conv_launch {
+  const int64_t *conv_addrs;
+  const int64_t *conv_block_strides;
+  const int64_t *conv_dim_strides;
+  const int64_t *conv_token_strides;
+  int64_t conv_dim;
+  int64_t history;
+  int64_t window;
+  int32_t element_bytes;
+  int32_t reserved;
+} gdn_conv_launch;
+
+/* Plan-array entries (plan->num_groups * plan->plan_capacity) that
+ * gdn_recoverssm_commit_noalloc holds: 8 groups of 4096 rows. */
+#define GDN_NOALLOC_PLAN_ENTRIES 32768
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc):
+ * the commit of gdn_recoverssm_plan_fold followed by gdn_recoverssm_conv_compact
+ * (when `conv` is not NULL), with the seven plan arrays held in a buffer the
+ * library owns on each GPU (7 x GDN_NOALLOC_PLAN_ENTRIES int32, 896 KiB,
+ * kept until the process ends) instead of arrays the caller allocates. The
+ * plan-array pointers of `plan` must be NULL; everything else has the meaning
+ * and the checks of gdn_recoverssm_plan_fold (and of the conv compaction, with
+ * config[1] layers and config[5] blocks), and pages, conv states and the align
+ * publication come out identical. num_groups * plan_capacity above
+ * GDN_NOALLOC_PLAN_ENTRIES is rejected before anything runs. The plan stays in
+ * the library, so publication across buckets (gdn_recoverssm_publish) is not
+ * available through this entry; GDN_PLAN_PUBLISH within one plan is. Every
+ * call on a GPU shares that GPU's buffer: calls that overlap on one GPU (on
+ * different streams, or from different threads without ordering) race. The
+ * stream must belong to the current device. Nothing is allocated: the first
+ * call on a device only looks the buffer's address up. */
+int gdn_recoverssm_commit_noalloc(const gdn_plan_launch *plan, void *state_ref, const void *correction_ref,
+                                  const void *key_ref, const void *decay_ref, const int64_t *state_addrs,
+                                  const int64_t *state_block_strides, const int64_t *corr_addrs,
+                                  const int64_t *corr_block_strides, const int64_t *key_addrs,
+                                  const int64_t *key_block_strides, const int64_t *decay_addrs,
+                                  const int64_t *decay_block_strides, const int32_t *layer_groups,
+                                  const int64_t *config, int64_t config_len, const gdn_fold_ext *ext,
+                                  const gdn_conv_launch *conv, void *stream);
+
 /* Conv-state compaction (grouped_commit.py:225-322 / kernels.py:1075-1169).
  * Per-layer DEVICE tables: base addresses, block / dim / token strides
  * (elements). element_bytes is 2 or 4. `source` as in gdn_recoverssm_fold.

@@ -89,6 +89,29 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert st == N.GDN_ERR_INVALID and b"differ from the plan" in lib.gdn_recoverssm_last_error()
 
 
+def test_commit_noalloc_rejects_before_touching_the_device():
+    """The no-allocation commit refuses caller plan arrays and a plan larger
+    than the library's buffer before any HIP call (none is possible here)."""
+    lib = N.load()
+    groups = N.PlanGroups()
+    fext = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1)
+    cfg = N.i64_array([4, 1, 4, 2, 4, 16, 4, 8, 0, 128 * 128, 128, 512, 128, 256, 128, 4, 1])
+
+    def call(launch, conv=None):
+        return lib.gdn_recoverssm_commit_noalloc(ctypes.byref(launch), None, None, None, None, *([8] * 8), None, cfg,
+                                                 17, ctypes.byref(fext), conv, None)
+
+    base = dict(sampled=8, sampled_len=4, sampled_dtype=3, num_groups=1,
+                groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), num_rows=4, spec_query_len=4)
+    st = call(N.PlanLaunch(**base, plan_capacity=8, lens_plan=8))
+    assert st == N.GDN_ERR_INVALID and b"pass NULL" in lib.gdn_recoverssm_last_error()
+    st = call(N.PlanLaunch(**dict(base, num_groups=2), plan_capacity=N.NOALLOC_PLAN_ENTRIES // 2 + 1))
+    assert st == N.GDN_ERR_INVALID and b"exceed" in lib.gdn_recoverssm_last_error()
+    st = call(N.PlanLaunch(**base, plan_capacity=8), ctypes.byref(N.ConvLaunch(conv_dim=40, history=3, window=6,
+                                                                              element_bytes=2)))
+    assert st == N.GDN_ERR_INVALID and b"conv_compact" in lib.gdn_recoverssm_last_error()
+
+
 def test_zero_rows_is_a_noop_without_touching_the_device():
     lib = N.load()
     ext = N.VerifyExt(key_dim=128, value_dim=128, act_dtype=1, out_dtype=1, state_dtype=0, key_record_dtype=1,
@@ -109,6 +132,10 @@ int main(void) {
   printf("gdn_gating_ext %zu\n", sizeof(gdn_gating_ext));
   printf("gdn_pending_commit %zu\n", sizeof(gdn_pending_commit));
   printf("gdn_plan_launch %zu\n", sizeof(gdn_plan_launch));
+  printf("gdn_conv_launch %zu\n", sizeof(gdn_conv_launch));
+  printf("noalloc_entries %d\n", GDN_NOALLOC_PLAN_ENTRIES);
+  F(gdn_conv_launch, conv_token_strides) F(gdn_conv_launch, conv_dim) F(gdn_conv_launch, window)
+  F(gdn_conv_launch, element_bytes)
   F(gdn_plan_launch, groups) F(gdn_plan_launch, col_plan) F(gdn_plan_launch, idx_mapping_dtype)
   F(gdn_plan_launch, flags) F(gdn_plan_launch, persistent_len) F(gdn_plan_launch, spec_query_len)
   F(gdn_pending_commit, record_rows) F(gdn_pending_commit, decay_strides) F(gdn_pending_commit, key_per_value_head)
@@ -137,13 +164,15 @@ def test_ctypes_struct_layout_matches_c_compiler():
     assert int(got["gdn_gating_ext"]) == ctypes.sizeof(N.GatingExt)
     assert int(got["gdn_pending_commit"]) == ctypes.sizeof(N.PendingCommit)
     assert int(got["gdn_plan_launch"]) == ctypes.sizeof(N.PlanLaunch)
+    assert int(got["gdn_conv_launch"]) == ctypes.sizeof(N.ConvLaunch)
+    assert int(got.pop("noalloc_entries")) == N.NOALLOC_PLAN_ENTRIES
     for key, value in got.items():
         if "." not in key:
             continue
         struct, fld = key.split(".")
         cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup,
                "gdn_gating_ext": N.GatingExt, "gdn_pending_commit": N.PendingCommit,
-               "gdn_plan_launch": N.PlanLaunch}[struct]
+               "gdn_plan_launch": N.PlanLaunch, "gdn_conv_launch": N.ConvLaunch}[struct]
         assert getattr(cls, fld).offset == int(value), key
 
 
