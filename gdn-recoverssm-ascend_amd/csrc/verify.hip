@@ -55,9 +55,10 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     set_error("verify: %lld rows exceed the 65535-row grid", (long long)rows);
     return GDN_ERR_UNSUPPORTED;
   }
-  for (int i : {17, 18, 20, 21, 23, 24}) {
+  // Every stride and count the kernel takes in 32 bits.
+  for (int i : {5, 7, 8, 9, 10, 11, 12, 13, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27}) {
     if (!fits_i32(config[i])) {
-      set_error("verify: record stride %d out of range", i);
+      set_error("verify: config field %d (%lld) exceeds 32 bits", i, (long long)config[i]);
       return GDN_ERR_UNSUPPORTED;
     }
   }
@@ -82,7 +83,9 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   }
   if (pending) {
     const bool ok = pending->record_rows > 0 && pending->num_rows > 0 && pending->num_rows <= INT32_MAX &&
-                    act_or_f32(pending->key_dtype) && fits_i32(pending->corr_strides[1]) &&
+                    act_or_f32(pending->key_dtype) && fits_i32(pending->corr_strides[0]) &&
+                    fits_i32(pending->key_strides[0]) && fits_i32(pending->decay_strides[0]) &&
+                    fits_i32(pending->corr_strides[1]) &&
                     fits_i32(pending->corr_strides[2]) && fits_i32(pending->key_strides[1]) &&
                     fits_i32(pending->key_strides[2]) && fits_i32(pending->decay_strides[1]) &&
                     fits_i32(pending->decay_strides[2]) &&
@@ -120,29 +123,29 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   a.heads = int32_t(heads);
   a.value_heads = int32_t(value_heads);
   a.Q = int32_t(Q);
-  a.blocks = blocks;
+  a.blocks = int32_t(blocks);
   a.record_rows = int32_t(record_rows);
-  a.null_block = null_block;
-  a.q_ts = config[8];
-  a.k_ts = config[9];
-  a.v_ts = config[10];
-  a.g_ts = config[11];
-  a.beta_ts = config[12];
-  a.state_bs = state_bs;
+  a.null_block = int32_t(null_block);
+  a.q_ts = int32_t(config[8]);
+  a.k_ts = int32_t(config[9]);
+  a.v_ts = int32_t(config[10]);
+  a.g_ts = int32_t(config[11]);
+  a.beta_ts = int32_t(config[12]);
+  a.state_bs = int32_t(state_bs);
   a.state_hs = int32_t(state_hs);
   a.state_vs = int32_t(state_vs);
-  a.corr_rs = config[16];
+  a.corr_rs = int32_t(config[16]);
   a.corr_hs = int32_t(config[17]);
   a.corr_ts = int32_t(config[18]);
-  a.key_rs = config[19];
+  a.key_rs = int32_t(config[19]);
   a.key_hs = int32_t(config[20]);
   a.key_ts = int32_t(config[21]);
-  a.decay_rs = config[22];
+  a.decay_rs = int32_t(config[22]);
   a.decay_hs = int32_t(config[23]);
   a.decay_ts = int32_t(config[24]);
-  a.out_ts = config[25];
-  a.qsl_s = config[26];
-  a.idx_s = config[27];
+  a.out_ts = int32_t(config[25]);
+  a.qsl_s = int32_t(config[26]);
+  a.idx_s = int32_t(config[27]);
   a.scale = scale;
   a.K = int32_t(K);
   a.V = int32_t(V);
@@ -174,13 +177,13 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     a.p_corr = static_cast<const float *>(pending->correction);
     a.p_key = pending->key;
     a.p_decay = static_cast<const float *>(pending->decay);
-    a.p_corr_rs = pending->corr_strides[0];
+    a.p_corr_rs = int32_t(pending->corr_strides[0]);
     a.p_corr_hs = int32_t(pending->corr_strides[1]);
     a.p_corr_ts = int32_t(pending->corr_strides[2]);
-    a.p_key_rs = pending->key_strides[0];
+    a.p_key_rs = int32_t(pending->key_strides[0]);
     a.p_key_hs = int32_t(pending->key_strides[1]);
     a.p_key_ts = int32_t(pending->key_strides[2]);
-    a.p_decay_rs = pending->decay_strides[0];
+    a.p_decay_rs = int32_t(pending->decay_strides[0]);
     a.p_decay_hs = int32_t(pending->decay_strides[1]);
     a.p_decay_ts = int32_t(pending->decay_strides[2]);
     a.p_key_f32 = pending->key_dtype == GDN_DT_F32;

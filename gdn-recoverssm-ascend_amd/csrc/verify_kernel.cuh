@@ -45,10 +45,12 @@ struct VerifyArgs {
   float *decay;
   void *out;
   const void *qsl, *indices;
-  int64_t state_bs, q_ts, k_ts, v_ts, g_ts, beta_ts;
-  int64_t corr_rs, key_rs, decay_rs, out_ts;
-  int64_t qsl_s, idx_s;
-  int64_t blocks, null_block;
+  // Element strides and page counts fit in 32 bits (checked on the host);
+  // every product with a row, token or page index is formed in 64 bits.
+  int32_t state_bs, q_ts, k_ts, v_ts, g_ts, beta_ts;
+  int32_t corr_rs, key_rs, decay_rs, out_ts;
+  int32_t qsl_s, idx_s;
+  int32_t blocks, null_block;
   int32_t tokens, heads, value_heads, Q, record_rows;
   int32_t state_hs, state_vs;
   int32_t corr_hs, corr_ts, key_hs, key_ts, decay_hs, decay_ts;
@@ -67,7 +69,7 @@ struct VerifyArgs {
   const int32_t *p_rows, *p_src, *p_len, *p_final, *p_bnd, *p_blen;
   const float *p_corr, *p_decay;
   const void *p_key;
-  int64_t p_corr_rs, p_key_rs, p_decay_rs;
+  int32_t p_corr_rs, p_key_rs, p_decay_rs;
   int32_t p_corr_hs, p_corr_ts, p_key_hs, p_key_ts, p_decay_hs, p_decay_ts;
   int32_t p_key_f32, p_key_per_value_head, p_record_rows, p_num_rows;
 };
@@ -276,57 +278,52 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   }
   const int64_t qlen = eos - bos;
   const int64_t out_base = int64_t(hv) * V + row0;
-  // Token validity is uniform across the wave (kernels.py:612).
-  uint32_t valid_mask = 0;
-#pragma unroll
-  for (int t = 0; t < QM; ++t) {
-    const int64_t tok = bos + t;
-    if (t < Q && t < qlen && tok >= 0 && tok < a.tokens) valid_mask |= 1u << t;
+  // Token validity is uniform across the wave (kernels.py:612): lane t < QM
+  // tests token t and one ballot gathers the window's mask (an unrolled test
+  // per token became a chain of scalar branches).
+  uint32_t valid_mask;
+  {
+    const int64_t tok = bos + lane;
+    const bool tv = lane < QM && lane < Q && lane < qlen && tok >= 0 && tok < a.tokens;
+    valid_mask = uint32_t(__builtin_amdgcn_ballot_w64(tv));
   }
 
   // ---- 1. gates (and DEFER: the pending plan and decays): one load ----
   // Lane t < QM reads the dword holding g of token t, lane QM + t that of
-  // beta (FP32, or the 16-bit value at its half); tokens outside the window
-  // read the first word of query_start_loc (always present; g and beta may be
-  // empty, hence null, when the launch has no token at all) and are
-  // discarded. DEFER: lanes 2QM .. 2QM+4 read the pending row's accepted
-  // length, source, final and boundary pages and boundary length, and lanes
-  // 2QM+5 .. 3QM+4 its decays; a row without a pending row reads row 0
-  // (num_rows >= 1) and discards it. The ordinary kernel waits for these
-  // words only after its state loads issue; the deferred one needs the
-  // pending source page first.
+  // beta (FP32, or the 16-bit value at its half); every address is formed on
+  // its own lane. Tokens outside the window read the first word of
+  // query_start_loc (always present; g and beta may be empty, hence null,
+  // when the launch has no token at all) and are discarded. DEFER: lanes
+  // 2QM .. 2QM+4 read the pending row's accepted length, source, final and
+  // boundary pages and boundary length, and lanes 2QM+5 .. 3QM+4 its decays;
+  // a row without a pending row reads row 0 (num_rows >= 1) and discards it.
+  // The ordinary kernel waits for these words only after its state loads
+  // issue; the deferred one needs the pending source page first.
   const int gsz = a.g_f32 ? 4 : AS, bsz = a.beta_f32 ? 4 : AS;
   const uintptr_t any_word = reinterpret_cast<uintptr_t>(a.qsl);
-  int gsh[QM], bsh[QM];
+  const bool gate_lane_b = lane >= QM;          // lanes QM .. 2QM-1 carry beta
+  const int gate_t = (gate_lane_b ? lane - QM : lane) & 31;
+  int gate_sh;                                   // bit offset of this lane's 16-bit gate in its word
   uint32_t gw;
   const bool prow_ok = DEFER && prow >= 0 && prow < a.p_num_rows && prow < a.p_record_rows;
   const int pr = prow_ok ? prow : 0;
   {
-    uintptr_t addr = any_word;
-#pragma unroll
-    for (int t = 0; t < QM; ++t) {
-      const bool tv = (valid_mask >> t) & 1u;
-      const uintptr_t ga =
-          tv ? reinterpret_cast<uintptr_t>(a.g) + uintptr_t(((bos + t) * a.g_ts + hv) * gsz) : any_word;
-      const uintptr_t ba =
-          tv ? reinterpret_cast<uintptr_t>(a.beta) + uintptr_t(((bos + t) * a.beta_ts + hv) * bsz) : any_word;
-      gsh[t] = int(ga & 2) * 8;
-      bsh[t] = int(ba & 2) * 8;
-      addr = lane == t ? ga : addr;
-      addr = lane == QM + t ? ba : addr;
-    }
+    const bool tv = lane < 2 * QM && ((valid_mask >> gate_t) & 1u);
+    const uintptr_t base = reinterpret_cast<uintptr_t>(gate_lane_b ? a.beta : a.g);
+    const int64_t ts = gate_lane_b ? a.beta_ts : a.g_ts;
+    const int64_t sz = gate_lane_b ? bsz : gsz;
+    uintptr_t addr = tv ? base + uintptr_t(((bos + gate_t) * ts + hv) * sz) : any_word;
+    gate_sh = int(addr & 2) * 8;
     if constexpr (DEFER) {
       const int32_t *plan[5] = {a.p_len, a.p_src, a.p_final, a.p_bnd, a.p_blen};
 #pragma unroll
       for (int i = 0; i < 5; ++i)
         addr = lane == 2 * QM + i ? reinterpret_cast<uintptr_t>(plan[i] + pr) : addr;
-#pragma unroll
-      for (int t = 0; t < QM; ++t) {
-        const uintptr_t da = reinterpret_cast<uintptr_t>(a.p_decay) +
-                             uintptr_t((int64_t(pr) * a.p_decay_rs + int64_t(hv) * a.p_decay_hs +
-                                        int64_t(t) * a.p_decay_ts) * 4);
-        addr = lane == 2 * QM + 5 + t ? (t < Q ? da : any_word) : addr;
-      }
+      const int dt = lane - (2 * QM + 5);
+      const uintptr_t da = reinterpret_cast<uintptr_t>(a.p_decay) +
+                           uintptr_t((int64_t(pr) * a.p_decay_rs + int64_t(hv) * a.p_decay_hs +
+                                      int64_t(dt) * a.p_decay_ts) * 4);
+      addr = dt >= 0 && dt < QM ? (dt < Q ? da : any_word) : addr;
     }
     gw = lane_word(addr & ~uintptr_t(3));
   }
@@ -407,9 +404,11 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     const int idx = p * kVerifyThreads + lane;
     const int vid = idx / C4, kk = (idx - vid * C4) * 4;
     const bool is_q = vid >= QM;
-    const int t = is_q ? vid - QM : vid;
-    const bool live = vid < NV && ((valid_mask >> t) & 1u) && kk < K;
-    const int el = t * int(is_q ? a.q_ts : a.k_ts) + h * K + kk;
+    const int t = (is_q ? vid - QM : vid) & 31;
+    // Non-short-circuit tests: a short-circuit chain became a branch per pass,
+    // with kernel arguments reloaded inside it.
+    const bool live = (vid < NV) & (((valid_mask >> t) & 1u) != 0) & (kk < K);
+    const int el = t * (is_q ? a.q_ts : a.k_ts) + h * K + kk;
     const int off = live ? el * AS : kOutOfRange;
     if constexpr (C4 * QM % kVerifyThreads == 0) {
       // Every pass lies wholly inside the k vectors or wholly inside the q ones.
@@ -430,7 +429,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
       const int vr = row0 + half * 64 + lane;
-      const bool ok = vr < V && ((valid_mask >> t) & 1u);
+      const bool ok = (vr < V) & (((valid_mask >> t) & 1u) != 0);
       const int off = ok ? (t * int(a.v_ts) + int(out_base) + half * 64 + lane) * AS : kOutOfRange;
       vv[half][t] = buf_ld_act<A>(rv, off);
     }
@@ -496,22 +495,29 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     neg_a = -expf(scalar_param<A>(a.a_log, hv, a.a_log_dt));
     dtb = scalar_param<A>(a.dt_bias, hv, a.dt_bias_dt);
   }
-#pragma unroll
-  for (int t = 0; t < QM; ++t) {
-    const bool tv = (valid_mask >> t) & 1u;
-    const uint32_t graw = word_of(gw, t), braw = word_of(gw, QM + t);
-    float gv = a.g_f32 ? __uint_as_float(graw) : bits_to_f32<A>((graw >> gsh[t]) & 0xffffu);
-    float bv = a.beta_f32 ? __uint_as_float(braw) : bits_to_f32<A>((braw >> bsh[t]) & 0xffffu);
+  {
+    // Each gate lane decodes its own word; the window's decays and betas then
+    // reach every lane by readlane.
+    const bool f32 = gate_lane_b ? a.beta_f32 != 0 : a.g_f32 != 0;
+    float x = f32 ? __uint_as_float(gw) : bits_to_f32<A>((gw >> gate_sh) & 0xffffu);
     if (a.gated) {
       // docs/reference/recoverssm_gdn_upstream.py:135-151
-      const float x = gv + dtb;
-      const float bx = a.softplus_beta * x;
-      const float sp = bx <= a.softplus_threshold ? log1pf(expf(bx)) / a.softplus_beta : x;
-      gv = neg_a * sp;
-      bv = 1.0f / (1.0f + expf(-bv));
+      if (gate_lane_b) {
+        x = 1.0f / (1.0f + expf(-x));
+      } else {
+        const float xb = x + dtb;
+        const float bx = a.softplus_beta * xb;
+        const float sp = bx <= a.softplus_threshold ? log1pf(expf(bx)) / a.softplus_beta : xb;
+        x = neg_a * sp;
+      }
     }
-    dec[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? expf(gv) : 1.0f)));
-    bet[t] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tv ? bv : 0.0f)));
+    const float gate = gate_lane_b ? x : expf(x);
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const bool tv = (valid_mask >> t) & 1u;
+      dec[t] = tv ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gate), t)) : 1.0f;
+      bet[t] = tv ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gate), QM + t)) : 0.0f;
+    }
   }
 
   // ---- 4. stage vectors and records ----
