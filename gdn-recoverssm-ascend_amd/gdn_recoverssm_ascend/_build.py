@@ -24,6 +24,8 @@ INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libgdn_recoverssm_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+# The source digest of a built library, written beside it by build().
+DIGEST_SUFFIX = ".digest"
 ARCH = os.environ.get("GDN_OFFLOAD_ARCH", "gfx950")
 
 
@@ -69,9 +71,11 @@ def compile_flags() -> list[str]:
 
 
 def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str:
-    """Compile every source (in parallel, largest first) and link the shared library."""
+    """Compile every source (in parallel, largest first), link the shared
+    library and record the digest of the sources it was built from beside it."""
     from concurrent.futures import ThreadPoolExecutor
 
+    digest = source_digest()
     os.makedirs(LIB_DIR, exist_ok=True)
     cc = hipcc()
     srcs = sorted(sources(), key=os.path.getsize, reverse=True)
@@ -104,7 +108,18 @@ def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str
         if r.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + r.stdout.decode(errors="replace"))
         os.replace(tmp_lib, LIB_PATH)
+    with open(LIB_PATH + DIGEST_SUFFIX, "w") as f:
+        f.write(digest + "\n")
     return LIB_PATH
+
+
+def built_digest(path: str) -> str | None:
+    """The source digest recorded beside a built library (None when absent)."""
+    try:
+        with open(path + DIGEST_SUFFIX) as f:
+            return f.read().strip()
+    except OSError:
+        return None
 
 
 if __name__ == "__main__":

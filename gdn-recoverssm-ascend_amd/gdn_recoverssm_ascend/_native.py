@@ -13,7 +13,7 @@ import threading
 
 import torch
 
-from ._build import LIB_PATH
+from ._build import CSRC_DIR, LIB_PATH, built_digest, source_digest
 
 ABI_VERSION = 1
 VERIFY_CONFIG_FIELDS = 28
@@ -172,6 +172,7 @@ def load() -> ctypes.CDLL:
                 f"GDN RecoverSSM HIP library not found at {path}; build it with "
                 "`python -m gdn_recoverssm_ascend._build` (there is no fallback path)"
             )
+        _refuse_stale(path)
         lib = ctypes.CDLL(path)
         lib.gdn_recoverssm_abi_version.restype = ctypes.c_int
         lib.gdn_recoverssm_abi_version.argtypes = []
@@ -222,6 +223,24 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"GDN RecoverSSM HIP library ABI mismatch: {version} != {ABI_VERSION}")
         _LIB = lib
     return _LIB
+
+
+def _refuse_stale(path: str) -> None:
+    """Refuse a library built from other kernel sources than the ones beside
+    the package. The in-tree library must carry the digest build() records;
+    a library named by GDN_RECOVERSSM_HIP_LIB is checked when it carries one."""
+    recorded = built_digest(path)
+    if recorded is None and os.path.abspath(path) != os.path.abspath(LIB_PATH):
+        return
+    if not os.path.isdir(CSRC_DIR):
+        return  # an installed library without its sources: nothing to compare against
+    current = source_digest()
+    if recorded != current:
+        raise RuntimeError(
+            f"GDN RecoverSSM HIP library at {path} was built from other kernel sources "
+            f"(recorded digest {recorded or 'missing'}, sources {current}); rebuild it with "
+            "`python -m gdn_recoverssm_ascend._build` (there is no fallback path)"
+        )
 
 
 def exported_symbols() -> tuple[str, ...]:

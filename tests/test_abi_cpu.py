@@ -196,6 +196,38 @@ def test_native_caller_is_built_against_this_header():
     assert r.returncode == 2 and b"usage" in r.stdout
 
 
+def test_stale_library_is_refused(tmp_path):
+    """A library whose recorded source digest differs from the kernel sources
+    beside the package is refused at load, as is the in-tree library without
+    a recorded digest; the in-tree build carries the current digest. Run in a
+    child process, since the library loads once per process."""
+    import shutil
+
+    from gdn_recoverssm_ascend import _build
+
+    assert _build.built_digest(LIB_PATH) == _build.source_digest(), "rebuild: the in-tree library is stale"
+    stale = tmp_path / "libstale.so"
+    shutil.copy(LIB_PATH, stale)
+    (tmp_path / "libstale.so.digest").write_text("0" * 40 + "\n")
+    code = (
+        "from gdn_recoverssm_ascend import _native\n"
+        "try:\n"
+        "    _native.load()\n"
+        "except RuntimeError as e:\n"
+        "    assert 'other kernel sources' in str(e), str(e)\n"
+        "else:\n"
+        "    raise SystemExit('a stale library loaded')\n"
+        "print('ok')\n"
+    )
+    pkg = os.path.dirname(os.path.dirname(N.__file__))
+    env = dict(os.environ, GDN_RECOVERSSM_HIP_LIB=str(stale),
+               PYTHONPATH=pkg + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    r = subprocess.run([sys.executable, "-c", code], env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       timeout=300)
+    out = r.stdout.decode(errors="replace")
+    assert r.returncode == 0 and out.strip().endswith("ok"), out
+
+
 def test_missing_library_fails_loudly(tmp_path):
     """With the HIP library absent, the first call into the package raises
     RuntimeError naming the missing path: there is no CPU fallback to fall
