@@ -33,7 +33,9 @@ def pointer_table(tensors: Sequence[torch.Tensor], device, byte_offset: int = 0)
 
 
 def stride_table(tensors: Sequence[torch.Tensor], dim: int, device) -> torch.Tensor:
-    return torch.tensor([t.stride(dim) for t in tensors], dtype=torch.int64, device=device)
+    """int64 device table of each tensor's element stride along ``dim``."""
+    strides = torch.as_tensor([t.stride()[dim] for t in tensors], dtype=torch.int64)
+    return strides.to(device)
 
 
 @dataclass(frozen=True)

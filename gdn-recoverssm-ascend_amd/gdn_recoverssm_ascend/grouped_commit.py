@@ -95,13 +95,11 @@ class _Unshared:
 
 
 def _rows_of(entry: CommitEntry):
-    p = entry.payload
-    rows = int(p.state_indices.shape[0])
-    request_rows = tuple(getattr(p, "request_rows", ()))
-    query_lens = tuple(getattr(p, "query_lens", ()))
-    if len(request_rows) != rows or len(query_lens) != rows:
+    payload = entry.payload
+    evidence = tuple(tuple(getattr(payload, name, ())) for name in ("request_rows", "query_lens"))
+    if any(len(e) != len(payload.state_indices) for e in evidence):
         return _Unshared(id(entry.metadata))
-    return _LogicalRows(request_rows, query_lens, p.block_size, p.block_table is not None)
+    return _LogicalRows(*evidence, payload.block_size, payload.block_table is not None)
 
 
 def _partition(entries: list) -> list:
@@ -124,14 +122,15 @@ def _publisher_descriptors(buckets) -> torch.Tensor:
     one int64 device table, cached on the first bucket while the same plan
     arrays are in use; the cache keeps those arrays (only them) alive."""
     owner = buckets[0]
-    identity = tuple((id(b.valid), id(b.col), b.capacity, len(b.contexts)) for b in buckets)
-    if getattr(owner, "_publisher_identity", None) != identity:
-        words = [w for b in buckets for w in (b.valid.data_ptr(), b.col.data_ptr(), b.capacity, len(b.contexts))]
-        words = [w - (1 << 64) if w >= (1 << 63) else w for w in words]
-        owner._publisher_table = torch.tensor(words, dtype=torch.int64, device=owner.device)
-        owner._publisher_arrays = tuple((b.valid, b.col) for b in buckets)
-        owner._publisher_identity = identity
-    return owner._publisher_table
+    # The table's own words identify it: the same plan arrays, capacities and
+    # group counts give the same words.
+    words = tuple(w for b in buckets for w in (b.valid.data_ptr(), b.col.data_ptr(), b.capacity, len(b.contexts)))
+    cached = owner.__dict__.get("_publisher")
+    if cached is None or cached[0] != words:
+        signed = [w - (1 << 64) if w >= (1 << 63) else w for w in words]
+        table = torch.tensor(signed, dtype=torch.int64, device=owner.device)
+        owner._publisher = (words, table, tuple((b.valid, b.col) for b in buckets))
+    return owner._publisher[1]
 
 
 def _publish_spec(buckets, request_indices, idx_mapping, persistent_cols, persistent_accepted, rows) -> _LaunchSpec:
@@ -206,12 +205,14 @@ class GroupedCommitBucket:
         self.num_key_heads = int(first.num_key_heads)
         self.key_dtype = first.key_dtype
         self.conv_history_len = int(first.conv_history_len)
-        self.max_blocks = max(int(c.num_blocks) for c in contexts)
+        self.max_blocks = int(max(c.num_blocks for c in contexts))
         self.pages = LayerPages([t for c in contexts for t in c.conv_states],
                                 [t for c in contexts for t in c.checkpoints],
                                 [t for c in contexts for t in c.records], self.device)
-        self.layer_groups = torch.tensor([g for g, c in enumerate(contexts) for _ in c.checkpoints],
-                                         dtype=torch.int32, device=self.device)
+        # Each layer's group: context g's layers all map to plan group g.
+        per_context = torch.tensor([len(c.checkpoints) for c in contexts])
+        self.layer_groups = torch.repeat_interleave(torch.arange(len(contexts), dtype=torch.int32),
+                                                    per_context).to(self.device)
         # Plan arrays: group g's row r at g * capacity + r.
         for name in ("source", "length", "final", "boundary", "boundary_len", "valid", "col"):
             setattr(self, name, torch.zeros(self.capacity * len(contexts), dtype=torch.int32, device=self.device))
@@ -228,11 +229,11 @@ class GroupedCommitBucket:
         if len(entries) != len(self.contexts) or any(e.context is not c for e, c in zip(entries, self.contexts)):
             fail("grouped recovery bucket belongs to a different KV epoch")
         payloads = tuple(e.payload for e in entries)
-        rows = int(payloads[0].state_indices.shape[0])
-        if not 0 < rows <= self.capacity:
-            fail("grouped recovery rows out of range: "
-                 f"rows={rows}, record capacity={self.capacity}, groups={len(payloads)}, state_indices shapes="
-                 f"{[tuple(p.state_indices.shape) for p in payloads]}")
+        rows = len(payloads[0].state_indices)
+        if rows < 1 or rows > self.capacity:
+            shapes = [tuple(p.state_indices.shape) for p in payloads]
+            fail(f"grouped recovery rows out of range: rows={rows}, record capacity={self.capacity}, "
+                 f"groups={len(payloads)}, state_indices shapes={shapes}")
         enforce(_bucket_rules(self, entries, payloads, rows, sampled, idx_mapping, persistent_cols,
                               persistent_accepted))
         align = payloads[0].block_table is not None
@@ -278,16 +279,13 @@ class GroupedCommitBucket:
 
 def _step_entries(metadata) -> list:
     """The cache groups of a step that carry a RecoverSSM commit."""
-    entries = []
-    for m in metadata:
-        payload = getattr(m, "recoverssm_commit", None)
-        if payload is None or getattr(m, "recoverssm_builder", None) is None:
-            continue
-        context = getattr(m, "recoverssm_context", None)
-        if context is None:
-            raise RuntimeError("a serving RecoverSSM commit has no producer binding epoch")
-        entries.append(CommitEntry(m, payload, context))
-    return entries
+    def carries_commit(m) -> bool:
+        return all(getattr(m, name, None) is not None for name in ("recoverssm_commit", "recoverssm_builder"))
+
+    committing = [m for m in metadata if carries_commit(m)]
+    if any(getattr(m, "recoverssm_context", None) is None for m in committing):
+        raise RuntimeError("a serving RecoverSSM commit has no producer binding epoch")
+    return [CommitEntry(m, m.recoverssm_commit, m.recoverssm_context) for m in committing]
 
 
 def _check_step(entries) -> bool:
@@ -315,28 +313,30 @@ class GroupedCommitCoordinator:
     epoch's pages are not held."""
 
     def __init__(self):
-        self._buckets = {}
-        self._seen = set()
+        self._buckets: dict = {}        # context identities -> bucket, the last step's only
+        self._logged_shapes: set = set()
         self.steps = 0
-        self.last_launch_count = 0
-        self.last_group_count = 0
-        self.last_rows = 0
+        self._note_step(0, 0, 0)
+
+    def _note_step(self, launches: int, groups: int, rows: int) -> None:
+        """The last step's diagnostics: launches issued, groups committed, rows."""
+        self.last_launch_count, self.last_group_count, self.last_rows = launches, groups, rows
 
     def _bucket_for(self, members) -> GroupedCommitBucket:
         contexts = tuple(e.context for e in members)
-        epoch = tuple(id(c) for c in contexts)
-        bucket = self._buckets.get(epoch)
-        if bucket is None:
-            prepared = getattr(members[0].metadata.recoverssm_builder, "_prepared_group_bucket", None)
-            adoptable = prepared is not None and len(prepared.contexts) == len(contexts) and all(
-                a is b for a, b in zip(prepared.contexts, contexts))
-            bucket = prepared if adoptable else GroupedCommitBucket(contexts)
-        return bucket
+        key = tuple(map(id, contexts))
+        if key in self._buckets:
+            return self._buckets[key]
+        # A bucket built by prepare_grouped_commit for exactly these contexts is adopted.
+        prepared = getattr(members[0].metadata.recoverssm_builder, "_prepared_group_bucket", None)
+        if prepared is not None and tuple(map(id, prepared.contexts)) == key:
+            return prepared
+        return GroupedCommitBucket(contexts)
 
     def commit(self, metadata, sampled, idx_mapping, persistent_cols, persistent_accepted):
         entries = _step_entries(metadata)
         if not entries:
-            self.last_launch_count = self.last_group_count = self.last_rows = 0
+            self._note_step(0, 0, 0)
             return
         align = _check_step(entries)
         buckets = _partition(entries)
@@ -350,7 +350,7 @@ class GroupedCommitCoordinator:
             for spec in specs:
                 spec.launch()
             launches += len(specs)
-        rows = int(entries[0].payload.state_indices.shape[0])
+        rows = len(entries[0].payload.state_indices)
         if align and len(buckets) > 1:
             # The plans of every bucket are stored now: publish where all agree.
             _publish_spec(tuple(used.values()), entries[0].payload.request_indices, idx_mapping, persistent_cols,
@@ -358,13 +358,11 @@ class GroupedCommitCoordinator:
             launches += 1
         self._buckets = used
         self.steps += 1
-        self.last_launch_count = launches
-        self.last_group_count = len(entries)
-        self.last_rows = rows
-        shape = (len(entries), len(buckets))
-        if shape not in self._seen:
-            self._seen.add(shape)
-            logger.info("GDN recovery coordinator: groups=%d buckets=%d launches=%d", *shape, launches)
+        self._note_step(launches, len(entries), rows)
+        shape = (len(entries), len(buckets), launches)
+        if shape not in self._logged_shapes:  # once per step shape
+            self._logged_shapes.add(shape)
+            logger.info("grouped RecoverSSM commit: %d cache groups in %d buckets, %d launches", *shape)
 
 
 # ---------------------------------------------------------------------------
@@ -387,11 +385,13 @@ def _probe_payload(builder, context, block_tables, num_computed_tokens, device):
         (1, window), dtype=torch.int32, device=device)
     block_table = computed = block_size = None
     if align:
-        group_id = getattr(builder, "_gdn_kv_cache_group_id", None)
-        bound = getattr(block_tables, "input_block_tables", None)
-        if bound is None or group_id is None or not 0 <= group_id < len(bound):
+        try:  # the builder's cache group selects its table among the bound native tables
+            gid = int(builder._gdn_kv_cache_group_id)
+            block_table = block_tables.input_block_tables[gid][:1] if gid >= 0 else None
+        except (AttributeError, TypeError, IndexError):
+            block_table = None
+        if block_table is None:
             raise RuntimeError("grouped align preparation requires the bound native group table")
-        block_table = bound[group_id][:1]
         computed = num_computed_tokens[:1] if num_computed_tokens is not None else torch.zeros(
             1, dtype=torch.int32, device=device)
         block_size = int(builder.kv_cache_spec.block_size)

@@ -24,6 +24,7 @@ on the current stream, and a failed launch raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
+import math
 from collections import Counter
 from collections.abc import Sequence
 from dataclasses import dataclass, field, replace
@@ -83,31 +84,20 @@ class ReplayRecordBuffers:
     key: torch.Tensor
     decay: torch.Tensor
 
+    # Views derived from the three planes (the attribute names the callers use).
+    planes = property(lambda self: (self.correction, self.key, self.decay))
+    device = property(lambda self: self.correction.device)
+    key_dtype = property(lambda self: self.key.dtype)
+    num_key_heads = property(lambda self: int(self.key.shape[1]))
+    dtype = property(lambda self: torch.float32, doc="Arithmetic type of the records (FP32 whatever the key dtype).")
+    record_bytes = property(lambda self: sum(p.numel() * p.element_size() for p in self.planes))
+
     @property
     def shape(self) -> tuple[int, int, int, int]:
-        """The logical packed shape, (rows, HV, Q, V + K + 1)."""
-        rows, heads, window, value_dim = self.correction.shape
-        return (rows, heads, window, value_dim + self.key.shape[-1] + 1)
-
-    @property
-    def dtype(self):
-        return torch.float32
-
-    @property
-    def device(self):
-        return self.correction.device
-
-    @property
-    def num_key_heads(self) -> int:
-        return int(self.key.shape[1])
-
-    @property
-    def key_dtype(self):
-        return self.key.dtype
-
-    @property
-    def record_bytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (self.correction, self.key, self.decay))
+        """The packed layout this record set stands for: one [V | K | 1] row per
+        (record row, value head, token)."""
+        *lead, v = self.correction.shape
+        return (*lead, v + self.key.shape[-1] + 1)
 
     @classmethod
     def allocate(cls, rows: int, num_value_heads: int, num_key_heads: int, window: int, value_dim: int,
@@ -340,23 +330,25 @@ def _run_verify(c: _VerifyCall, scale, out, _collect, *, pending=None) -> torch.
     """Checks, output allocation, the early return on an empty batch, the
     kernel checks, then the launch (or its spec into ``_collect``)."""
     _check_verify(c)
-    if scale is None:
-        scale = c.K ** -0.5
-    if out is None:
-        out = torch.empty(1, c.tokens, c.HV, c.V, dtype=c.v.dtype, device=c.v.device)
-    require(tuple(out.shape) == (1, c.tokens, c.HV, c.V) and out.stride()[2:] == (c.V, 1),
-            "output shape or layout is incompatible")
+    want = (1, c.tokens, c.HV, c.V)
+    out = torch.empty(want, dtype=c.v.dtype, device=c.v.device) if out is None else out
+    require(tuple(out.shape) == want and out.stride()[2:] == (c.V, 1), "output shape or layout is incompatible")
     # Nothing to verify: done, unless pending commits still have to be applied.
-    if c.rows == 0 or (c.tokens == 0 and pending is None):
-        return out
-    c.out = out
-    enforce(_kernel_rules(c))
-    spec = _verify_spec(c, out, scale, pending=pending)
-    if _collect is None:
-        spec.launch()
-    else:
-        _collect.append(spec)
+    idle = c.rows == 0 or (c.tokens == 0 and pending is None)
+    if not idle:
+        c.out = out
+        enforce(_kernel_rules(c))
+        # The default scale is the reference's 1 / sqrt(K).
+        _submit(_verify_spec(c, out, math.pow(c.K, -0.5) if scale is None else scale, pending=pending), _collect)
     return out
+
+
+def _submit(spec: "_LaunchSpec", collect: list | None) -> None:
+    """Launch now, or hand the spec to a caller that collects them."""
+    if collect is not None:
+        collect.append(spec)
+        return
+    spec.launch()
 
 
 def gdn_recoverssm_verify(
@@ -692,11 +684,20 @@ def _commit_rules(ctx, accepted, state_indices, qsl, request_indices, block_tabl
         ("align block size must cover one speculative window",
          lambda: block_size is None or block_size >= ctx.spec_query_len),
         ("block table must be two-dimensional with a positive width",
-         lambda: block_table is None or (block_table.ndim == 2 and block_table.shape[1] > 0)),
+         lambda: block_table is None or (block_table.dim() == 2 and block_table.size(-1) >= 1)),
         ("commit inputs must be on the same device",
          lambda: all(t is None or t.device == device for t in tensors)),
         ("the commit runs on a HIP device", lambda: device.type == "cuda"),
     )
+
+
+def _conv_dim_first_default() -> bool:
+    """Conv pages are channel-major unless an installed vLLM says otherwise."""
+    try:
+        from vllm.model_executor.layers.mamba.mamba_utils import is_conv_state_dim_first
+    except ImportError:
+        return True
+    return bool(is_conv_state_dim_first())
 
 
 class GDNRecoverSSMCommitContext:
@@ -758,8 +759,8 @@ class GDNRecoverSSMCommitContext:
     ) -> "GDNRecoverSSMCommitContext":
         """Bind the layers' pages and records (conv states token-major when
         ``conv_dim_first`` is false) and allocate the plan arrays."""
-        if not conv_dim_first:
-            conv_states = [s.transpose(-1, -2) for s in conv_states]
+        # Token-major conv pages are viewed channel-major: the kernels take strides.
+        conv_states = list(conv_states) if conv_dim_first else [c.mT for c in conv_states]
         typed = [isinstance(r, ReplayRecordBuffers) for r in replays]
         require(all(typed) or not any(typed), "packed and typed records cannot share a commit context")
         check_layers(conv_states, checkpoints, replays, window=spec_query_len, typed=bool(typed and typed[0]),
@@ -789,26 +790,18 @@ class GDNRecoverSSMCommitContext:
         they are allocated here, ``record_rows`` (default ``max_num_reqs``)
         rows per layer, and handed to each layer as
         ``layer._gdn_recoverssm_records`` for its verify to write."""
-        if conv_dim_first is None:
-            try:  # vLLM decides the conv layout when it is installed
-                from vllm.model_executor.layers.mamba.mamba_utils import is_conv_state_dim_first
-
-                conv_dim_first = bool(is_conv_state_dim_first())
-            except ImportError:
-                conv_dim_first = True
-        if any(len(layer.kv_cache) != 2 for layer in layers):
+        caches = [tuple(layer.kv_cache) for layer in layers]
+        if {len(c) for c in caches} != {2}:
             raise ValueError("GDN RecoverSSM expects conv and checkpoint pages; the replay records live outside the cache")
-        pages0 = layers[0].kv_cache[1]
-        _, HV, V, K = pages0.shape
-        records = [
-            ReplayRecordBuffers.allocate(int(record_rows or max_num_reqs), HV,
-                                         HV if num_key_heads is None else int(num_key_heads), spec_query_len, V, K,
-                                         device=pages0.device, key_dtype=key_dtype or torch.float32)
-            for _ in layers
-        ]
-        context = cls.from_tensors([layer.kv_cache[0] for layer in layers], [layer.kv_cache[1] for layer in layers],
-                                   records, spec_query_len=spec_query_len, max_num_reqs=max_num_reqs,
-                                   conv_dim_first=conv_dim_first)
+        conv_pages, state_pages = (list(pages) for pages in zip(*caches))
+        _, HV, V, K = state_pages[0].shape
+        rows = int(record_rows or max_num_reqs)
+        key_heads = HV if num_key_heads is None else int(num_key_heads)
+        records = [ReplayRecordBuffers.allocate(rows, HV, key_heads, spec_query_len, V, K, device=state_pages[0].device,
+                                                key_dtype=key_dtype or torch.float32) for _ in caches]
+        layout = _conv_dim_first_default() if conv_dim_first is None else conv_dim_first
+        context = cls.from_tensors(conv_pages, state_pages, records, spec_query_len=spec_query_len,
+                                   max_num_reqs=max_num_reqs, conv_dim_first=layout)
         for layer, record in zip(layers, records):
             layer._gdn_recoverssm_records = record
         return context
@@ -829,9 +822,8 @@ class GDNRecoverSSMCommitContext:
     ) -> tuple:
         """The launch specs of one step's commit, not launched."""
         specs: list = []
-        self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices=request_indices,
-                    block_table=block_table, num_computed_tokens=num_computed_tokens,
-                    mamba_block_size=mamba_block_size, commit_conv=commit_conv, _collect=specs)
+        self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices, block_table,
+                    num_computed_tokens, mamba_block_size, commit_conv, specs)
         return tuple(specs)
 
     def prepare_verify(self, *, activation_dtype, state_table_width: int | None = None, device=None) -> list:
@@ -839,7 +831,7 @@ class GDNRecoverSSMCommitContext:
         a page: a contiguous and a combined-QKV value view (the fused
         projection's token stride), each with an FP32 and an activation-typed
         beta; one report dict per signature."""
-        device = self.checkpoints[0].device if device is None else device
+        device = device or self.checkpoints[0].device
         _, HV, V, K = self.checkpoints[0].shape
         H, Q = self.num_key_heads, self.spec_query_len
         width = int(state_table_width or Q)
@@ -853,20 +845,21 @@ class GDNRecoverSSMCommitContext:
         table, offsets = blank(1, width, dtype=torch.int32), blank(2, dtype=torch.int32)
         fused = blank(1, Q, 2 * H * K + HV * V)
         value_views = {False: blank(1, Q, HV, V), True: fused[:, :, 2 * H * K:].view(1, Q, HV, V)}
+        # What every signature of this epoch shares, then one entry per signature.
+        epoch = {"activation_dtype": str(activation_dtype), "state_index_stride": width,
+                 "state_blocks": self.num_blocks, "record_rows": self.record_rows, "num_value_heads": HV,
+                 "num_key_heads": H, "window": Q}
+        signatures = [(value, beta_dtype) for value in value_views.values()
+                      for beta_dtype in dict.fromkeys((torch.float32, activation_dtype))]
         report = []
-        for combined, value in value_views.items():
-            for beta_dtype in dict.fromkeys((torch.float32, activation_dtype)):
-                specs: list = []
-                gdn_recoverssm_verify(g, blank(1, Q, HV, dtype=beta_dtype), q, k, value,
-                                      checkpoint_state=self.checkpoints[0], replay_cache=self.records[0],
-                                      query_start_loc=offsets, state_indices=table[:, 0], spec_query_len=Q,
-                                      qk_already_normalized=True, out=out, _collect=specs)
-                for spec in specs:
-                    spec.compile_only()
-                report.append(dict(activation_dtype=str(activation_dtype), beta_dtype=str(beta_dtype),
-                                   value_token_stride=value.stride(1), state_index_stride=width,
-                                   state_blocks=self.num_blocks, record_rows=self.record_rows, num_value_heads=HV,
-                                   num_key_heads=H, window=Q))
+        for value, beta_dtype in signatures:
+            specs: list = []
+            gdn_recoverssm_verify(g, blank(1, Q, HV, dtype=beta_dtype), q, k, value,
+                                  checkpoint_state=self.checkpoints[0], replay_cache=self.records[0],
+                                  query_start_loc=offsets, state_indices=table[:, 0], spec_query_len=Q,
+                                  qk_already_normalized=True, out=out, _collect=specs)
+            _ = [spec.compile_only() for spec in specs]
+            report.append({**epoch, "beta_dtype": str(beta_dtype), "value_token_stride": value.stride(1)})
         self.verify_prepare_report = tuple(report)
         return report
 
@@ -888,25 +881,24 @@ class GDNRecoverSSMCommitContext:
     ) -> list[int]:
         """Check the none / align commit signature for every batch size up to
         ``capacity`` (and the record rows); returns the row counts checked."""
-        require(not align_mode or (mamba_block_size is not None and mamba_block_size >= self.spec_query_len),
+        require(not align_mode or (mamba_block_size or 0) >= self.spec_query_len,
                 "align preparation requires the runtime block size")
         width = int(block_table_width or state_table_width)
-        checked = []
-        for rows in range(1, min(capacity, self.record_rows) + 1):
-            def blank(*shape, dtype):
-                return torch.empty(shape, dtype=dtype, device=device)
 
-            align = dict(block_table=blank(rows, width, dtype=state_index_dtype),
-                         num_computed_tokens=blank(rows, dtype=computed_dtype),
-                         mamba_block_size=mamba_block_size) if align_mode else {}
-            specs = self.make_commit_specs(
-                blank(rows, dtype=accepted_dtype), blank(rows, state_table_width, dtype=state_index_dtype)[:, 0],
-                blank(rows + 1, dtype=query_index_dtype),
-                request_indices=blank(rows, dtype=request_index_dtype) if request_mapping else None, **align)
-            for spec in specs:
-                spec.compile_only()
-            checked.append(rows)
-        return checked
+        def blank(shape, dtype):
+            return torch.empty(shape, dtype=dtype, device=device)
+
+        def signature(n: int) -> tuple:
+            """Placeholder commit inputs of n rows with the serving dtypes and strides."""
+            return (blank(n, accepted_dtype), blank((n, state_table_width), state_index_dtype)[:, 0],
+                    blank(n + 1, query_index_dtype), blank(n, request_index_dtype) if request_mapping else None,
+                    blank((n, width), state_index_dtype) if align_mode else None,
+                    blank(n, computed_dtype) if align_mode else None, mamba_block_size if align_mode else None)
+
+        batch_sizes = list(range(1, min(capacity, self.record_rows) + 1))
+        for n in batch_sizes:
+            _ = [spec.compile_only() for spec in self.make_commit_specs(*signature(n))]
+        return batch_sizes
 
     # -- the commit --
 
@@ -993,10 +985,8 @@ class GDNRecoverSSMCommitContext:
         last step, or rows whose requests left)."""
         require(self.record_layout == "soa", "the deferred commit needs typed record buffers")
         specs: list = []
-        self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices=request_indices,
-                    block_table=block_table, num_computed_tokens=num_computed_tokens,
-                    mamba_block_size=mamba_block_size, commit_conv=commit_conv, _collect=specs,
-                    _fold_source=self.plan_source)
+        self.commit(num_accepted_tokens, state_indices, query_start_loc, request_indices, block_table,
+                    num_computed_tokens, mamba_block_size, commit_conv, specs, _fold_source=self.plan_source)
         self._deferred_fold = next(sp for sp in specs if sp.name == "fold")
         self._deferred_rows = int(state_indices.shape[0])
         now = [sp for sp in specs if sp.name != "fold"]
