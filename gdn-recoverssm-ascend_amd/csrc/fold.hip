@@ -69,9 +69,12 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   constexpr int ITERS = 64 / E;  // chunks held per thread per batch (64 f32 values)
   extern __shared__ float lds[];
 
-  const int64_t hv = w % a.heads;
-  const int64_t row = (w / a.heads) % a.rows;
-  const int64_t layer = w / (a.heads * a.rows);
+  // 32-bit division: the grid is below 2^31 workgroups (checked on the host),
+  // and a 64-bit division here became a long inline sequence per index.
+  const uint32_t wu = uint32_t(w), heads = uint32_t(a.heads), rows = uint32_t(a.rows);
+  const int64_t hv = wu % heads;
+  const int64_t row = (wu / heads) % rows;
+  const int64_t layer = wu / (heads * rows);
   const int64_t group = a.layer_groups ? int64_t(a.layer_groups[layer]) : 0;
   const int64_t plan_row = group * a.cap + row;
   int64_t src, fin, bidx;
@@ -83,7 +86,7 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
     // group the plan does not cover folds nothing.
     if (group < 0 || group >= p->num_groups) return;
     const gdn_plan_group &g = p->groups[group];
-    pr = plan_begin(*p, g, row);
+    pr = plan_begin_lanes(*p, g, row);
     src = pr.source;
     n = int(pr.count);
     if (!(plan_may_commit(*p, g, pr) && src > a.null_block && src < a.blocks && n <= a.Q && row < a.record_rows))
@@ -125,7 +128,7 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   for (int i = 0; i < ITERS; ++i) raw[i] = load_stream(rsrc, voff, i * step);
   if constexpr (PLANNED) {
     const gdn_plan_group &g = p->groups[group];
-    plan_finish(*p, g, pr);
+    plan_finish_lanes(*p, g, pr);
     if (!(pr.valid && pr.final_idx > a.null_block && pr.final_idx < a.blocks)) return;
     fin = pr.final_idx;
     bidx = pr.boundary;

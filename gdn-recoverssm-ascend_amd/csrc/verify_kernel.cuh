@@ -197,29 +197,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Wave-uniform words gathered by one vector load: every lane reads the 32-bit
-// word at its own address and readlane hands lane i's word to the whole wave.
-// A wave's offsets, slot, gates and pending plan are read this way, a few
-// words per lane-indexed load and one wait each, instead of one load and one
-// wait per word: as separate loads the compiler issued each only after the
-// previous one returned, and three serial round trips under the load of the
-// other waves' state streams took a third of a wave's life before its first
-// state load could issue.
-// Through the global address space: a flat load would also count against the
-// LDS / scalar counter, and every LDS wait would then wait for it.
-__device__ __forceinline__ uint32_t lane_word(uintptr_t addr) {
-  return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t *>(addr);
-}
-__device__ __forceinline__ uint32_t word_of(uint32_t w, int i) { return uint32_t(__builtin_amdgcn_readlane(int(w), i)); }
-// int32 or int64 element from its low and high words (for int32 the high
-// word is a second read of the low one).
-__device__ __forceinline__ int64_t index_of(uint32_t lo, uint32_t hi, bool i64) {
-  return i64 ? int64_t((uint64_t(hi) << 32) | lo) : int64_t(int32_t(lo));
-}
-__device__ __forceinline__ uintptr_t elem_addr(const void *p, int64_t i, bool i64) {
-  return reinterpret_cast<uintptr_t>(p) + uintptr_t(i) * (i64 ? 8u : 4u);
-}
-
 // DEFER: before verifying, apply the previous step's commit for this row (the
 // fold of kernels.py:1222-1324, folded into the next verify): the state comes
 // from the pending commit's source page, its accepted prefix is replayed from
