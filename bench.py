@@ -157,6 +157,116 @@ def measured_traffic(workload, kernel):
     return k["hbm_bytes"], os.path.relpath(path, HERE)
 
 
+def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
+    """Synthetic twins of the step's two kernels (csrc/probe/traffic_probe.hip):
+    the verify's state tiles, small reads and output / record writes, and the
+    fold's tile copies (source page -> final and boundary pages, written into a
+    scratch pool with the workload's page layout), moved in each kernel's own
+    access pattern with no arithmetic, timed as a step (verify twin, then fold
+    twin, an event between them) as the kernels are. The twin's time is what
+    the memory system sustains for that traffic; kernel_over_twin is the
+    kernel's time over it."""
+    import ctypes
+
+    import torch
+
+    from gdn_recoverssm_ascend import _build
+
+    if not os.path.exists(_build.PROBE_LIB_PATH):
+        return {"note": f"{_build.PROBE_LIB_PATH} not built"}
+    lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.gdn_probe_verify_twin.argtypes = [vp, vp, i64, vp, i64, vp, i64, vp, vp]
+    lib.gdn_probe_fold_twin.argtypes = [vp, vp, vp, vp, vp, i64, vp]
+    s = w.spec
+    B, HV, H, K, V = s.rows, s.value_heads, s.key_heads, s.key_dim, s.value_dim
+    if (K, V) != (128, 128) or w.checkpoints[0].dtype != torch.float32:
+        return {"note": "the twins model 64 KiB FP32 tiles (K = V = 128)"}
+    dev = w.checkpoints[0].device
+    ck = w.checkpoints[0]
+    tile = V * K * 4
+    page_b, head_b = ck.stride(0) * 4, ck.stride(1) * 4
+    idx = w.meta.state_indices.cpu().long()
+    rows = idx[(idx > 0) & (idx < w.num_pages)]
+    hv = torch.arange(HV)
+    tiles = (rows[:, None] * page_b + hv[None, :] * head_b).reshape(-1).to(dev)
+    n_v = tiles.numel()
+    T = nbytes["tokens"]
+    writes = T * HV * V * (2 + 4) + T * H * K * 2 + T * HV * 4
+    small = nbytes["verify"] - n_v * tile - writes
+    small_dw = max(0, small // 4 // max(1, (n_v + 1) // 2))  # read once per wave pair (q, k shared)
+    write_dw = writes // 4 // n_v
+    small_buf = torch.zeros(((n_v + 1) // 2) * small_dw + 1, dtype=torch.float32, device=dev)
+    wbuf = torch.empty(n_v * write_dw + 1, dtype=torch.float32, device=dev)
+    sink = torch.empty(n_v, dtype=torch.float32, device=dev)
+    n, fin, bnd, blen = (t.cpu().long()[:B] for t in plan)
+    src = w.meta.state_indices.cpu().long()
+    act = n > 0
+    store_b = act & (bnd > 0) & (bnd < w.num_pages) & (bnd != fin) & (blen > 0) & (blen <= n)
+    so = (src[act][:, None] * page_b + hv[None, :] * head_b).reshape(-1)
+    do = (fin[act][:, None] * page_b + hv[None, :] * head_b).reshape(-1)
+    d2 = torch.where(store_b[act][:, None], bnd[act][:, None] * page_b + hv[None, :] * head_b,
+                     torch.full((1, HV), -1, dtype=torch.long)).reshape(-1)
+    so, do, d2 = so.to(dev), do.to(dev), d2.to(dev)
+    n_f = so.numel()
+    pool = torch.empty_like(ck)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def vtwin(sdw=small_dw, wdw=write_dw):
+        st = lib.gdn_probe_verify_twin(ck.data_ptr(), tiles.data_ptr(), n_v, small_buf.data_ptr(), sdw,
+                                       wbuf.data_ptr(), wdw, sink.data_ptr(), stream)
+        assert st == 0, f"verify twin: status {st}"
+
+    def ftwin():
+        st = lib.gdn_probe_fold_twin(ck.data_ptr(), pool.data_ptr(), so.data_ptr(), do.data_ptr(), d2.data_ptr(),
+                                     n_f, stream)
+        assert st == 0, f"fold twin: status {st}"
+
+    for _ in range(10):
+        vtwin()
+        ftwin()
+    marks = [[timer.event() for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for ev in marks:
+        timer.record(ev[0])
+        vtwin()
+        timer.record(ev[1])
+        ftwin()
+        timer.record(ev[2])
+    torch.cuda.synchronize()
+    v_us = sum(timer.elapsed(ev[0], ev[1]) for ev in marks) / steps * 1e3
+    f_us = sum(timer.elapsed(ev[1], ev[2]) for ev in marks) / steps * 1e3
+    r0, r1 = timer.event(), timer.event()
+    for _ in range(3):
+        vtwin(0, 0)
+    torch.cuda.synchronize()
+    timer.record(r0)
+    for _ in range(steps):
+        vtwin(0, 0)
+    timer.record(r1)
+    torch.cuda.synchronize()
+    ro_us = timer.elapsed(r0, r1) / steps * 1e3
+    v_bytes = n_v * tile + ((n_v + 1) // 2) * small_dw * 4 + n_v * write_dw * 4
+    f_bytes = n_f * tile * 2 + int(d2.ge(0).sum()) * tile
+    torch.cuda.synchronize()
+    del pool, wbuf, small_buf
+    torch.cuda.empty_cache()
+    return {
+        "verify_twin": {"us": round(v_us, 2), "bytes": v_bytes, "gbs": round(v_bytes / (v_us * 1e-6) / 1e9, 1),
+                        "reads_only_us": round(ro_us, 2),
+                        "reads_only_gbs": round(n_v * tile / (ro_us * 1e-6) / 1e9, 1),
+                        "kernel_us": round(kernel_us["verify"], 2),
+                        "kernel_over_twin": round(kernel_us["verify"] / v_us, 3)},
+        "fold_twin": {"us": round(f_us, 2), "bytes": f_bytes, "gbs": round(f_bytes / (f_us * 1e-6) / 1e9, 1),
+                      "kernel_us": round(kernel_us["plan_fold"], 2),
+                      "kernel_over_twin": round(kernel_us["plan_fold"] / f_us, 3)},
+        "note": "synthetic kernels moving the step's bytes in each kernel's access pattern with no arithmetic "
+                "(verify twin: the verify's state tiles, small reads and output / record writes; fold twin: the "
+                "committed tiles copied to their final and boundary pages of a scratch pool), timed as a step; "
+                "reads_only: the verify twin without its small reads and writes",
+    }
+
+
 def other_configs(args, timer, skip):
     """The verify + commit step of the other single-layer configurations
     (B=64 from a 512-page pool; B=256 at Q=1; B=256 at Q=8 with geometric
@@ -683,6 +793,10 @@ def main():
                     "ordinary step's algorithmic bytes by this step time",
         }
     gbs = total / (step_ms * 1e-3) / 1e9
+    ceiling = None
+    if not args.kernel_only:
+        plan4 = (ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
+        ceiling = traffic_ceiling(w, nbytes, plan4, {k: v * 1e3 for k, v in kernel_ms.items()}, timer, args.steps)
     others = None if args.kernel_only else other_configs(args, timer, s.name)
     # The 48-layer decode loop at its own size (its own 10 warmup steps, after
     # which the carried state restarts from the seeded start).
@@ -818,6 +932,7 @@ def main():
         "with_conv_compaction": full_step,
         "packed_records": packed,
         "deferred_commit": deferred,
+        "traffic_ceiling": ceiling,
         "other_configs": others,
         "decode_loop": loop,
     }

@@ -26,6 +26,10 @@ LIB_NAME = "libgdn_recoverssm_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 # The source digest of a built library, written beside it by build().
 DIGEST_SUFFIX = ".digest"
+# Synthetic traffic probes for bench.py's measured ceilings (not part of the
+# verify / commit path): a library of their own.
+PROBE_SRC = os.path.join(CSRC_DIR, "probe", "traffic_probe.hip")
+PROBE_LIB_PATH = os.path.join(LIB_DIR, "libgdn_recoverssm_probe.so")
 ARCH = os.environ.get("GDN_OFFLOAD_ARCH", "gfx950")
 
 
@@ -93,7 +97,8 @@ def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str
             return src, obj, r.returncode, text
 
         with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-            results = list(pool.map(compile_one, srcs))
+            results = list(pool.map(compile_one, srcs + [PROBE_SRC]))
+        probe = results.pop()
         errors = [f"{src}:\n{text}" for src, _, rc, text in results if rc != 0]
         if verbose:
             for src, _, rc, text in results:
@@ -108,6 +113,13 @@ def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str
         if r.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + r.stdout.decode(errors="replace"))
         os.replace(tmp_lib, LIB_PATH)
+        if probe[2] != 0:
+            raise RuntimeError(f"hipcc failed:\n{probe[0]}:\n{probe[3]}")
+        r = subprocess.run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", probe[1], "-o", PROBE_LIB_PATH + ".tmp"],
+                           stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        if r.returncode != 0:
+            raise RuntimeError("hipcc link failed:\n" + r.stdout.decode(errors="replace"))
+        os.replace(PROBE_LIB_PATH + ".tmp", PROBE_LIB_PATH)
     with open(LIB_PATH + DIGEST_SUFFIX, "w") as f:
         f.write(digest + "\n")
     return LIB_PATH
