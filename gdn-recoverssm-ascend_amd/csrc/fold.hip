@@ -128,7 +128,9 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   for (int i = 0; i < ITERS; ++i) raw[i] = load_stream(rsrc, voff, i * step);
   if constexpr (PLANNED) {
     const gdn_plan_group &g = p->groups[group];
-    plan_finish_lanes(*p, g, pr);
+    // Scalar reads: they return on the scalar counter while the state loads
+    // above are still in flight (a vector read here would wait for them all).
+    plan_finish(*p, g, pr);
     if (!(pr.valid && pr.final_idx > a.null_block && pr.final_idx < a.blocks)) return;
     fin = pr.final_idx;
     bidx = pr.boundary;
