@@ -112,6 +112,22 @@ def test_commit_noalloc_rejects_before_touching_the_device():
     assert st == N.GDN_ERR_INVALID and b"conv_compact" in lib.gdn_recoverssm_last_error()
 
 
+def test_verify_rejects_strides_beyond_32_bits():
+    """The kernel takes its element strides in 32 bits: a larger one is
+    refused on the host, before any HIP call."""
+    lib = N.load()
+    ext = N.VerifyExt(key_dim=128, value_dim=128, act_dtype=1, beta_dtype=0, g_dtype=0, state_dtype=0,
+                      key_record_dtype=1, qsl_dtype=3, index_dtype=3, out_dtype=1)
+    base = [1, 4, 1, 2, 4, 8, 1, 0, 256, 256, 256, 2, 2, 2 * 128 * 128, 128 * 128, 128, 2 * 4 * 128, 4 * 128, 128,
+            4 * 128, 4 * 128, 128, 2 * 4, 4, 1, 256, 1, 1]
+    for field in (8, 13, 16, 26):
+        cfg = list(base)
+        cfg[field] = 1 << 31
+        st = lib.gdn_recoverssm_verify(*([None] * 12), N.i64_array(cfg), 28, 1.0, ctypes.byref(ext), None)
+        assert st == N.GDN_ERR_UNSUPPORTED, field
+        assert f"config field {field}".encode() in lib.gdn_recoverssm_last_error(), lib.gdn_recoverssm_last_error()
+
+
 def test_zero_rows_is_a_noop_without_touching_the_device():
     lib = N.load()
     ext = N.VerifyExt(key_dim=128, value_dim=128, act_dtype=1, out_dtype=1, state_dtype=0, key_record_dtype=1,
