@@ -267,6 +267,23 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     }
 
 
+def kernel_times(specs, timer, steps):
+    """Each launch's average duration in us over `steps` steps, from HIP events
+    recorded between consecutive launches on the kernels' stream."""
+    import torch
+
+    marks = [[timer.event() for _ in range(len(specs) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for ev in marks:
+        timer.record(ev[0])
+        for j, sp in enumerate(specs):
+            sp.launch()
+            timer.record(ev[j + 1])
+    torch.cuda.synchronize()
+    return {sp.name: sum(timer.elapsed(ev[j], ev[j + 1]) for ev in marks) / steps * 1e3
+            for j, sp in enumerate(specs)}
+
+
 def other_configs(args, timer, skip):
     """The verify + commit step of the other single-layer configurations
     (B=64 from a 512-page pool; B=256 at Q=1; B=256 at Q=8 with geometric
@@ -313,9 +330,15 @@ def other_configs(args, timer, skip):
         nb = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices,
                         ctx.boundary_recovery_lens)
         total = nb["verify"] + nb["commit"]
+        kus = kernel_times(specs, timer, args.steps)
+        plan4 = (ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
+        twin = traffic_ceiling(w, nb, plan4, kus, timer, args.steps)
         res[name] = {"rows": B, "window": Q, "us_per_step": round(ms * 1e3, 2), "bytes": total,
                      "gbs": round(total / (ms * 1e-3) / 1e9, 1),
-                     "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                     "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "kernels_us": {k: round(v, 2) for k, v in kus.items()},
+                     "twins_us": {k: twin[k]["us"] for k in ("verify_twin", "fold_twin") if k in twin},
+                     "over_twin": {k: twin[k]["kernel_over_twin"] for k in ("verify_twin", "fold_twin") if k in twin}}
         del w, rec, ctx, out, specs
         torch.cuda.empty_cache()
     return res
