@@ -72,6 +72,52 @@ __device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int voff,
 constexpr int kEarlyPasses = 4;
 constexpr int64_t kEarlyMaxGrid = 4096;
 
+// The per-layer words a workgroup needs before its first state load: the
+// layer's plan group and its tile and record tables (state_addrs, state_bs,
+// corr_addrs, corr_bs, key_addrs, key_bs, decay_addrs, decay_bs at the layer).
+struct LayerRefs {
+  int64_t tab[8];
+  int64_t group;
+};
+// A planning workgroup gathers them with its plan words in one lane-indexed
+// load (lane kLayerLane: the group; the next 16 lanes: low and high words of
+// the eight tables), so its first state load waits for one round trip after
+// the kernel arguments instead of a chain of scalar reads.
+constexpr int kLayerLane = 10;
+__device__ __forceinline__ uintptr_t layer_lane_addr(const FoldArgs &a, int64_t layer, int lane, uintptr_t addr) {
+  const int64_t *const tabs[8] = {a.state_addrs, a.state_bs, a.corr_addrs, a.corr_bs,
+                                  a.key_addrs,   a.key_bs,   a.decay_addrs, a.decay_bs};
+  addr = (lane == kLayerLane) & (a.layer_groups != nullptr) ? reinterpret_cast<uintptr_t>(a.layer_groups + layer) : addr;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uintptr_t t = reinterpret_cast<uintptr_t>(tabs[i] + layer);
+    addr = lane == kLayerLane + 1 + 2 * i ? t : addr;
+    addr = lane == kLayerLane + 2 + 2 * i ? t + 4 : addr;
+  }
+  return addr;
+}
+__device__ __forceinline__ LayerRefs layer_refs_from(const FoldArgs &a, uint32_t w) {
+  LayerRefs L;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    L.tab[i] = index_of(word_of(w, kLayerLane + 1 + 2 * i), word_of(w, kLayerLane + 2 + 2 * i), true);
+  L.group = a.layer_groups ? int64_t(int32_t(word_of(w, kLayerLane))) : 0;
+  return L;
+}
+__device__ __forceinline__ LayerRefs layer_refs_load(const FoldArgs &a, int64_t layer) {
+  LayerRefs L;
+  L.tab[0] = a.state_addrs[layer];
+  L.tab[1] = a.state_bs[layer];
+  L.tab[2] = a.corr_addrs[layer];
+  L.tab[3] = a.corr_bs[layer];
+  L.tab[4] = a.key_addrs[layer];
+  L.tab[5] = a.key_bs[layer];
+  L.tab[6] = a.decay_addrs[layer];
+  L.tab[7] = a.decay_bs[layer];
+  L.group = a.layer_groups ? int64_t(a.layer_groups[layer]) : 0;
+  return L;
+}
+
 template <typename S, typename KT, bool PLANNED, bool EARLY>
 __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, int64_t w) {
   constexpr int E = Chunk<S>::E;
@@ -84,18 +130,26 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   const int64_t hv = wu % heads;
   const int64_t row = (wu / heads) % rows;
   const int64_t layer = wu / (heads * rows);
-  const int64_t group = a.layer_groups ? int64_t(a.layer_groups[layer]) : 0;
-  const int64_t plan_row = group * a.cap + row;
   int64_t src, fin, bidx;
   int n, blen;
   PlanRow pr;
+  LayerRefs L;
   if constexpr (PLANNED) {
     // The values gdn_recoverssm_plan would store for this (group, row), which
     // the fold below reads back under the same checks. A layer mapped to a
-    // group the plan does not cover folds nothing.
+    // group the plan does not cover folds nothing. The plan words are
+    // gathered for group 0 with the layer's words and gathered again for a
+    // layer of another group.
+    const gdn_plan_group &g0 = p->groups[0];
+    const int lane = int(threadIdx.x & 63);
+    uintptr_t addr = layer_lane_addr(a, layer, lane, reinterpret_cast<uintptr_t>(g0.query_start_loc));
+    addr = plan_lane_addr(*p, g0, row, lane, addr);
+    const uint32_t words = lane_word(addr);
+    L = layer_refs_from(a, words);
+    const int64_t group = L.group;
     if (group < 0 || group >= p->num_groups) return;
     const gdn_plan_group &g = p->groups[group];
-    pr = plan_begin_lanes(*p, g, row);
+    pr = group == 0 ? plan_from_words(*p, g0, row, words) : plan_begin_lanes(*p, g, row);
     src = pr.source;
     n = int(pr.count);
     if (!(plan_may_commit(*p, g, pr) && src > a.null_block && src < a.blocks && n <= a.Q && row < a.record_rows))
@@ -103,6 +157,8 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
     fin = bidx = a.null_block;
     blen = 0;
   } else {
+    L = layer_refs_load(a, layer);
+    const int64_t plan_row = L.group * a.cap + row;
     src = load_index(a.source, plan_row * a.source_stride, a.source_dtype);
     n = a.lengths[plan_row];
     fin = a.finals[plan_row];
@@ -113,8 +169,8 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
     blen = a.boundary_lens[plan_row];
   }
 
-  S *base = reinterpret_cast<S *>(a.state_addrs[layer]);
-  const int64_t sbs = a.state_bs[layer];
+  S *base = reinterpret_cast<S *>(L.tab[0]);
+  const int64_t sbs = L.tab[1];
   const int V = a.V;
   const int64_t vs = a.state_v_stride;
   const int tile_bytes = int(V * vs * int64_t(sizeof(S)));
@@ -134,9 +190,9 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   float early_c[EARLY ? kEarlyPasses : 1], early_k[EARLY ? kEarlyPasses : 1];
   if constexpr (EARLY) {
     // Branch-free: indices past the accepted tokens read as zero.
-    const float *cb = reinterpret_cast<const float *>(a.corr_addrs[layer]) + row * a.corr_bs[layer] +
+    const float *cb = reinterpret_cast<const float *>(L.tab[2]) + row * L.tab[3] +
                       hv * a.corr_head_stride;
-    const KT *kb = reinterpret_cast<const KT *>(a.key_addrs[layer]) + row * a.key_bs[layer] +
+    const KT *kb = reinterpret_cast<const KT *>(L.tab[4]) + row * L.tab[5] +
                    (hv / a.ratio) * a.key_head_stride;
     const __amdgpu_buffer_rsrc_t rc = fold_tile(cb, kFoldOutOfRange);
     const __amdgpu_buffer_rsrc_t rk = fold_tile(kb, kFoldOutOfRange);
@@ -160,7 +216,7 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
 #pragma unroll
   for (int i = 0; i < ITERS; ++i) raw[i] = load_stream(rsrc, voff, i * step);
   if constexpr (PLANNED) {
-    const gdn_plan_group &g = p->groups[group];
+    const gdn_plan_group &g = p->groups[L.group];
     // Scalar reads: they return on the scalar counter while the state loads
     // above are still in flight (a vector read here would wait for them all).
     plan_finish(*p, g, pr);
@@ -176,11 +232,11 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
 
   float *corr_lds = lds;                    // [n][V]
   float *key_lds = lds + a.Q * V;           // [n][KP]
-  const float *corr_base = reinterpret_cast<const float *>(a.corr_addrs[layer]) + row * a.corr_bs[layer] +
+  const float *corr_base = reinterpret_cast<const float *>(L.tab[2]) + row * L.tab[3] +
                            hv * a.corr_head_stride;
-  const KT *key_base = reinterpret_cast<const KT *>(a.key_addrs[layer]) + row * a.key_bs[layer] +
+  const KT *key_base = reinterpret_cast<const KT *>(L.tab[4]) + row * L.tab[5] +
                        (hv / a.ratio) * a.key_head_stride;
-  const float *decay_base = reinterpret_cast<const float *>(a.decay_addrs[layer]) + row * a.decay_bs[layer] +
+  const float *decay_base = reinterpret_cast<const float *>(L.tab[6]) + row * L.tab[7] +
                             hv * a.decay_head_stride;
   const int KP = a.KP;
   if constexpr (EARLY) {
@@ -239,8 +295,28 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   }
 }
 
+// Kernel arguments are read through the scalar cache, each where its value is
+// first needed, so a workgroup on a cold cache met one miss after another
+// (the fused launch's arguments span 28 lines of 64 bytes). Reading one word
+// of every line first, in one batch, makes that a single round trip (the B=64
+// fold 1 us shorter). Reads stay inside the BYTES the arguments occupy.
+template <int BYTES>
+__device__ __forceinline__ void warm_kernel_args() {
+  static_assert(BYTES <= 32 * 64, "argument block larger than the lines touched below");
+  const auto *k = (const __attribute__((address_space(4))) uint32_t *)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t w[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) w[i] = i * 64 < BYTES ? k[i * 16] : 0u;
+  // One consumer of every word: the reads are issued together and waited for once.
+  asm volatile("" ::"s"(w[0]), "s"(w[1]), "s"(w[2]), "s"(w[3]), "s"(w[4]), "s"(w[5]), "s"(w[6]), "s"(w[7]),
+               "s"(w[8]), "s"(w[9]), "s"(w[10]), "s"(w[11]), "s"(w[12]), "s"(w[13]), "s"(w[14]), "s"(w[15]),
+               "s"(w[16]), "s"(w[17]), "s"(w[18]), "s"(w[19]), "s"(w[20]), "s"(w[21]), "s"(w[22]), "s"(w[23]),
+               "s"(w[24]), "s"(w[25]), "s"(w[26]), "s"(w[27]), "s"(w[28]), "s"(w[29]), "s"(w[30]), "s"(w[31]));
+}
+
 template <typename S, typename KT, bool EARLY>
 __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
+  warm_kernel_args<int(sizeof(FoldArgs))>();
   fold_body<S, KT, false, EARLY>(a, nullptr, blockIdx.x);
 }
 
@@ -248,6 +324,7 @@ __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
 // fold, each planning its own row.
 template <typename S, typename KT, bool EARLY>
 __global__ __launch_bounds__(kFoldThreads) void plan_fold_kernel(FoldArgs a, PlanArgs p, int64_t writers) {
+  warm_kernel_args<int(sizeof(FoldArgs) + sizeof(PlanArgs) + sizeof(int64_t))>();
   const int64_t w = blockIdx.x;
   if (w < writers) {
     const int64_t row = w * kFoldThreads + threadIdx.x;

@@ -39,9 +39,9 @@ struct PlanRow {
 // Whether a request may be read: inside the accepted counts and, in align
 // mode, inside the block table and the computed-token counts.
 __device__ __forceinline__ bool plan_request_ok(const PlanArgs &a, const gdn_plan_group &g, int64_t request) {
-  bool ok = request >= 0 && request < a.sampled_len;
-  if (a.flags & GDN_PLAN_ALIGN) ok = ok && request < g.table_rows && request < g.computed_len;
-  return ok;
+  // Non-short-circuit: the bounds are read together, not behind branches.
+  const bool in_align = (request < g.table_rows) & (request < g.computed_len);
+  return (request >= 0) & (request < a.sampled_len) & (((a.flags & GDN_PLAN_ALIGN) == 0) | in_align);
 }
 
 // The first phase from the words it reads: the row's request, source page
@@ -93,21 +93,30 @@ __device__ __forceinline__ PlanRow plan_begin(const PlanArgs &a, const gdn_plan_
 // row itself), and one more for the accepted count and computed tokens of a
 // mapped request. Lanes with nothing to read read the first query offset,
 // which is always there. Same values as plan_begin.
-__device__ __forceinline__ PlanRow plan_begin_lanes(const PlanArgs &a, const gdn_plan_group &g, int64_t row) {
+//
+// plan_lane_addr gives lanes 0-9 their addresses (other lanes keep `addr`),
+// so that a caller can gather more words in the same load; plan_from_words
+// decodes the gathered word.
+__device__ __forceinline__ uintptr_t plan_lane_addr(const PlanArgs &a, const gdn_plan_group &g, int64_t row,
+                                                    int lane, uintptr_t addr) {
+  // Straight-line on purpose: every address is formed and then selected, so
+  // the kernel arguments behind them are read in one batch instead of each
+  // behind a branch of its own.
   const bool align = (a.flags & GDN_PLAN_ALIGN) != 0;
   const bool mapped = g.request_indices != nullptr;
-  const int lane = int(threadIdx.x & 63);
   const uintptr_t any = reinterpret_cast<uintptr_t>(g.query_start_loc);
   const bool s64 = g.si_dtype == GDN_DT_I64, q64 = g.qsl_dtype == GDN_DT_I64, m64 = g.map_dtype == GDN_DT_I64;
   const bool a64 = a.sampled_dtype == GDN_DT_I64, c64 = g.computed_dtype == GDN_DT_I64;
   const uintptr_t src = elem_addr(g.state_indices, row * g.si_stride, s64);
   const uintptr_t bos = elem_addr(g.query_start_loc, row * g.qsl_stride, q64);
   const uintptr_t eos = elem_addr(g.query_start_loc, (row + 1) * g.qsl_stride, q64);
-  const uintptr_t req = mapped ? elem_addr(g.request_indices, row * g.map_stride, m64) : any;
-  const bool row_ok = !mapped && plan_request_ok(a, g, row);
-  const uintptr_t acc = row_ok ? elem_addr(a.sampled, row * a.sampled_stride, a64) : any;
-  const uintptr_t cmp = row_ok && align ? elem_addr(g.num_computed, row * g.computed_stride, c64) : any;
-  uintptr_t addr = any;
+  const uintptr_t req_at = elem_addr(g.request_indices, row * g.map_stride, m64);
+  const uintptr_t acc_at = elem_addr(a.sampled, row * a.sampled_stride, a64);
+  const uintptr_t cmp_at = elem_addr(g.num_computed, row * g.computed_stride, c64);
+  const bool row_ok = !mapped & plan_request_ok(a, g, row);
+  const uintptr_t req = mapped ? req_at : any;
+  const uintptr_t acc = row_ok ? acc_at : any;
+  const uintptr_t cmp = row_ok & align ? cmp_at : any;
   addr = lane == 0 ? src : addr;
   addr = lane == 1 ? src + (s64 ? 4 : 0) : addr;
   addr = lane == 2 ? bos : addr;
@@ -115,13 +124,23 @@ __device__ __forceinline__ PlanRow plan_begin_lanes(const PlanArgs &a, const gdn
   addr = lane == 4 ? eos : addr;
   addr = lane == 5 ? eos + (q64 ? 4 : 0) : addr;
   addr = lane == 6 ? req : addr;
-  addr = lane == 7 ? req + (mapped && m64 ? 4 : 0) : addr;
+  addr = lane == 7 ? req + (mapped & m64 ? 4 : 0) : addr;
   addr = lane == 8 ? acc : addr;
   addr = lane == 9 ? cmp : addr;
-  const uint32_t w = lane_word(addr);
+  return addr;
+}
+
+__device__ __forceinline__ PlanRow plan_from_words(const PlanArgs &a, const gdn_plan_group &g, int64_t row,
+                                                   uint32_t w) {
+  const bool align = (a.flags & GDN_PLAN_ALIGN) != 0;
+  const bool mapped = g.request_indices != nullptr;
+  const int lane = int(threadIdx.x & 63);
+  const uintptr_t any = reinterpret_cast<uintptr_t>(g.query_start_loc);
+  const bool s64 = g.si_dtype == GDN_DT_I64, q64 = g.qsl_dtype == GDN_DT_I64, m64 = g.map_dtype == GDN_DT_I64;
+  const bool a64 = a.sampled_dtype == GDN_DT_I64, c64 = g.computed_dtype == GDN_DT_I64;
   const int64_t request = mapped ? index_of(word_of(w, 6), word_of(w, 7), m64) : row;
   int32_t accepted = int32_t(word_of(w, 8)), computed = int32_t(word_of(w, 9));
-  const bool ok = mapped ? plan_request_ok(a, g, request) : row_ok;
+  const bool ok = plan_request_ok(a, g, request);
   if (mapped) {
     const uintptr_t acc1 = ok ? elem_addr(a.sampled, request * a.sampled_stride, a64) : any;
     const uintptr_t cmp1 = ok && align ? elem_addr(g.num_computed, request * g.computed_stride, c64) : any;
@@ -132,6 +151,12 @@ __device__ __forceinline__ PlanRow plan_begin_lanes(const PlanArgs &a, const gdn
   return plan_begin_from(a, request, index_of(word_of(w, 0), word_of(w, 1), s64),
                          index_of(word_of(w, 2), word_of(w, 3), q64), index_of(word_of(w, 4), word_of(w, 5), q64), ok,
                          accepted, computed);
+}
+
+__device__ __forceinline__ PlanRow plan_begin_lanes(const PlanArgs &a, const gdn_plan_group &g, int64_t row) {
+  const int lane = int(threadIdx.x & 63);
+  const uintptr_t w = lane_word(plan_lane_addr(a, g, row, lane, reinterpret_cast<uintptr_t>(g.query_start_loc)));
+  return plan_from_words(a, g, row, w);
 }
 
 // Everything `valid` requires except the final page's range.
