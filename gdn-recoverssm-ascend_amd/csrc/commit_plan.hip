@@ -11,6 +11,7 @@
 namespace gdn {
 
 __global__ __launch_bounds__(64) void plan_kernel(PlanArgs a) {
+  warm_kernel_args<int(sizeof(PlanArgs))>();
   const int64_t row = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (row >= a.rows) return;
   plan_write_row(a, row);

@@ -295,25 +295,6 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   }
 }
 
-// Kernel arguments are read through the scalar cache, each where its value is
-// first needed, so a workgroup on a cold cache met one miss after another
-// (the fused launch's arguments span 28 lines of 64 bytes). Reading one word
-// of every line first, in one batch, makes that a single round trip (the B=64
-// fold 1 us shorter). Reads stay inside the BYTES the arguments occupy.
-template <int BYTES>
-__device__ __forceinline__ void warm_kernel_args() {
-  static_assert(BYTES <= 32 * 64, "argument block larger than the lines touched below");
-  const auto *k = (const __attribute__((address_space(4))) uint32_t *)__builtin_amdgcn_kernarg_segment_ptr();
-  uint32_t w[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) w[i] = i * 64 < BYTES ? k[i * 16] : 0u;
-  // One consumer of every word: the reads are issued together and waited for once.
-  asm volatile("" ::"s"(w[0]), "s"(w[1]), "s"(w[2]), "s"(w[3]), "s"(w[4]), "s"(w[5]), "s"(w[6]), "s"(w[7]),
-               "s"(w[8]), "s"(w[9]), "s"(w[10]), "s"(w[11]), "s"(w[12]), "s"(w[13]), "s"(w[14]), "s"(w[15]),
-               "s"(w[16]), "s"(w[17]), "s"(w[18]), "s"(w[19]), "s"(w[20]), "s"(w[21]), "s"(w[22]), "s"(w[23]),
-               "s"(w[24]), "s"(w[25]), "s"(w[26]), "s"(w[27]), "s"(w[28]), "s"(w[29]), "s"(w[30]), "s"(w[31]));
-}
-
 template <typename S, typename KT, bool EARLY>
 __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
   warm_kernel_args<int(sizeof(FoldArgs))>();
