@@ -32,6 +32,8 @@ struct FoldArgs {
   int64_t key_head_stride, key_token_stride;
   int64_t decay_head_stride, decay_token_stride;
   int32_t K, V, KP, KCH;  // KP: K padded to a whole number of chunks; KCH = KP / E
+  int32_t kp_log, kch_log;  // KP and KCH are powers of two
+  uint32_t v_magic;         // div16_magic(V)
   int32_t source_dtype;
 };
 
@@ -68,8 +70,8 @@ __device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int voff,
 // them, not for the tile behind them in the vector memory counter; for grids
 // of a few rounds of workgroups, where each workgroup's critical path shows
 // (1.8 us less for the B=64 step's fold; 1.6 us more at B=256, whose launch
-// the memory keeps busy anyway). Records of at most kEarlyPasses passes.
-constexpr int kEarlyPasses = 4;
+// the memory keeps busy anyway). Records of at most one batch.
+constexpr int kRecPasses = 4;  // workgroup passes per batch of record loads
 constexpr int64_t kEarlyMaxGrid = 4096;
 
 // The per-layer words a workgroup needs before its first state load: the
@@ -178,8 +180,8 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
 
   const int tid = threadIdx.x;
   const int KCH = a.KCH;
-  const int kc = tid % KCH;
-  const int r0 = tid / KCH;
+  const int kc = tid & (KCH - 1);
+  const int r0 = tid >> a.kch_log;
   const int RP = kFoldThreads / KCH;  // rows covered by one pass of the workgroup
   const bool kc_ok = kc * E < a.K;
   // Byte offset of the thread's chunk in pass 0 (rows past V fall outside the
@@ -187,30 +189,35 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   const int voff = kc_ok ? int((r0 * vs + kc * E) * int64_t(sizeof(S))) : kFoldOutOfRange;
   const int step = int(RP * vs * int64_t(sizeof(S)));
 
-  float early_c[EARLY ? kEarlyPasses : 1], early_k[EARLY ? kEarlyPasses : 1];
-  if constexpr (EARLY) {
-    // Branch-free: indices past the accepted tokens read as zero.
-    const float *cb = reinterpret_cast<const float *>(L.tab[2]) + row * L.tab[3] +
-                      hv * a.corr_head_stride;
-    const KT *kb = reinterpret_cast<const KT *>(L.tab[4]) + row * L.tab[5] +
-                   (hv / a.ratio) * a.key_head_stride;
-    const __amdgpu_buffer_rsrc_t rc = fold_tile(cb, kFoldOutOfRange);
-    const __amdgpu_buffer_rsrc_t rk = fold_tile(kb, kFoldOutOfRange);
+  // Records of the accepted tokens, corrections [n][V] and keys [n][KP] (zero
+  // past K), go to LDS. A batch covers kRecPasses passes of the workgroup;
+  // its loads are all issued before any is waited for, branch-free (indices
+  // past the accepted tokens read as zero). With EARLY the first batch is
+  // issued before the state tile, else after it; the host takes EARLY only
+  // when one batch holds all the records.
+  const float *corr_base = reinterpret_cast<const float *>(L.tab[2]) + row * L.tab[3] + hv * a.corr_head_stride;
+  const KT *key_base = reinterpret_cast<const KT *>(L.tab[4]) + row * L.tab[5] + (hv / a.ratio) * a.key_head_stride;
+  const __amdgpu_buffer_rsrc_t rcorr = fold_tile(corr_base, kFoldOutOfRange);
+  const __amdgpu_buffer_rsrc_t rkey = fold_tile(key_base, kFoldOutOfRange);
+  const int n_corr = n * a.V, n_key = n * a.KP;
+  auto load_records = [&](int first, float (&c)[kRecPasses], float (&k)[kRecPasses]) {
 #pragma unroll
-    for (int pp = 0; pp < kEarlyPasses; ++pp) {
-      const int idx = pp * kFoldThreads + int(threadIdx.x);
-      const int t = idx / a.V, v = idx - t * a.V;
-      const int coff = idx < n * a.V ? int((t * a.corr_token_stride + v) * 4) : kFoldOutOfRange;
-      early_c[pp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, coff, 0, 0));
-      const int tk = idx / a.KP, k = idx - tk * a.KP;
-      const int koff = idx < n * a.KP && k < a.K ? int((tk * a.key_token_stride + k) * int64_t(sizeof(KT)))
-                                                  : kFoldOutOfRange;
+    for (int pp = 0; pp < kRecPasses; ++pp) {
+      const int idx = first + pp * kFoldThreads + tid;
+      const int t = int(div16(uint32_t(idx), a.v_magic)), v = idx - t * a.V;
+      const int coff = idx < n_corr ? int((t * a.corr_token_stride + v) * 4) : kFoldOutOfRange;
+      c[pp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcorr, coff, 0, 0));
+      const int tk = idx >> a.kp_log, kk = idx & (a.KP - 1);
+      const int koff = idx < n_key && kk < a.K ? int((tk * a.key_token_stride + kk) * int64_t(sizeof(KT)))
+                                               : kFoldOutOfRange;
       if constexpr (sizeof(KT) == 4)
-        early_k[pp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, koff, 0, 0));
+        k[pp] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rkey, koff, 0, 0));
       else
-        early_k[pp] = to_f32(__builtin_bit_cast(KT, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rk, koff, 0, 0)));
+        k[pp] = to_f32(__builtin_bit_cast(KT, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rkey, koff, 0, 0)));
     }
-  }
+  };
+  float rec_c[kRecPasses], rec_k[kRecPasses];
+  if constexpr (EARLY) load_records(0, rec_c, rec_k);
   // Issue the first batch of state loads before staging the records.
   uint4 raw[ITERS];
 #pragma unroll
@@ -232,33 +239,36 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
 
   float *corr_lds = lds;                    // [n][V]
   float *key_lds = lds + a.Q * V;           // [n][KP]
-  const float *corr_base = reinterpret_cast<const float *>(L.tab[2]) + row * L.tab[3] +
-                           hv * a.corr_head_stride;
-  const KT *key_base = reinterpret_cast<const KT *>(L.tab[4]) + row * L.tab[5] +
-                       (hv / a.ratio) * a.key_head_stride;
-  const float *decay_base = reinterpret_cast<const float *>(L.tab[6]) + row * L.tab[7] +
-                            hv * a.decay_head_stride;
   const int KP = a.KP;
-  if constexpr (EARLY) {
+  auto stage_records = [&](int first) {
 #pragma unroll
-    for (int pp = 0; pp < kEarlyPasses; ++pp) {
-      const int idx = pp * kFoldThreads + tid;
-      if (idx < n * V) corr_lds[idx] = early_c[pp];
-      if (idx < n * KP) key_lds[idx] = early_k[pp];
+    for (int pp = 0; pp < kRecPasses; ++pp) {
+      const int idx = first + pp * kFoldThreads + tid;
+      if (idx < n_corr) corr_lds[idx] = rec_c[pp];
+      if (idx < n_key) key_lds[idx] = rec_k[pp];
     }
-  } else {
-    for (int idx = tid; idx < n * V; idx += kFoldThreads) {
-      const int t = idx / V, v = idx - t * V;
-      corr_lds[t * V + v] = corr_base[t * a.corr_token_stride + v];
-    }
-    for (int idx = tid; idx < n * KP; idx += kFoldThreads) {
-      const int t = idx / KP, k = idx - t * KP;
-      key_lds[t * KP + k] = k < a.K ? to_f32(key_base[t * a.key_token_stride + k]) : 0.0f;
-    }
+  };
+  if constexpr (!EARLY) load_records(0, rec_c, rec_k);
+  // The first batch is staged outside the loop: staged at a loop header, its
+  // waits would be counted for the loop's own loads, issued last, and so
+  // would wait for the state tile as well.
+  stage_records(0);
+  for (int first = kRecPasses * kFoldThreads; first < n_corr || first < n_key; first += kRecPasses * kFoldThreads) {
+    load_records(first, rec_c, rec_k);
+    stage_records(first);
   }
+  // Decays through the scalar path, clamped to the accepted tokens so every
+  // read is in bounds (the records are not written while the fold runs).
+  // Read as vector loads they would queue behind the state tile.
+  const uintptr_t decay_at = reinterpret_cast<uintptr_t>(reinterpret_cast<const float *>(L.tab[6]) + row * L.tab[7] +
+                                                          hv * a.decay_head_stride);
+  const auto *decay_ro = reinterpret_cast<const __attribute__((address_space(4))) float *>(decay_at);
   float decay[8];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) decay[t] = t < n ? decay_base[t * a.decay_token_stride] : 1.0f;
+  for (int t = 0; t < 8; ++t) {
+    const float d = decay_ro[(t < n ? t : n - 1) * a.decay_token_stride];
+    decay[t] = t < n ? d : 1.0f;
+  }
   __syncthreads();
 
   const int passes = (V + RP - 1) / RP;
@@ -419,10 +429,13 @@ static int make_fold_args(const int64_t *state_addrs, const int64_t *state_block
   a.decay_token_stride = config[16];
   a.K = int32_t(K);
   a.V = int32_t(V);
-  int kch = 1;
-  while (kch * E < K) kch *= 2;
+  int kch = 1, kch_log = 0;
+  while (kch * E < K) kch *= 2, ++kch_log;
   a.KCH = kch;
   a.KP = kch * E;
+  a.kch_log = kch_log;
+  a.kp_log = kch_log + (E == 8 ? 3 : E == 4 ? 2 : 1);
+  a.v_magic = div16_magic(uint32_t(V));
   *out = a;
   *grid = layers * rows * heads;
   *lds = size_t(query_len) * size_t(V + a.KP) * sizeof(float);
@@ -440,8 +453,8 @@ static int launch_fold(const gdn_fold_ext *ext, int64_t grid, size_t lds, const 
   // Records first for grids of a few rounds, when they fit the early passes
   // and their token windows the 32-bit offsets of a buffer resource.
   const int64_t key_bytes = ext->key_dtype == GDN_DT_F32 ? 4 : 2;
-  const bool early = grid <= kEarlyMaxGrid && a.Q * a.V <= kEarlyPasses * kFoldThreads &&
-                     a.Q * a.KP <= kEarlyPasses * kFoldThreads &&
+  const bool early = grid <= kEarlyMaxGrid && a.Q * a.V <= kRecPasses * kFoldThreads &&
+                     a.Q * a.KP <= kRecPasses * kFoldThreads &&
                      (a.Q * a.corr_token_stride + a.V) * 4 < kFoldOutOfRange &&
                      (a.Q * a.key_token_stride + a.KP) * key_bytes < kFoldOutOfRange && a.corr_token_stride >= 0 &&
                      a.key_token_stride >= 0;

@@ -94,9 +94,34 @@ __device__ __forceinline__ void warm_kernel_args() {
                "s"(w[24]), "s"(w[25]), "s"(w[26]), "s"(w[27]), "s"(w[28]), "s"(w[29]), "s"(w[30]), "s"(w[31]));
 }
 
+// Division by a runtime divisor d in [1, 2^16] of a dividend x < 2^16 as one
+// multiply-high: with m = floor(2^32 / d) + 1, m * d = 2^32 + e, 0 < e <= d,
+// so x * m / 2^32 = x / d + x * e / (d * 2^32) and the added term stays below
+// 1 / d (x * e < 2^32): the floor is exact. d = 1 (m would need 33 bits) is
+// coded as m = 0. A runtime division is otherwise about 15 vector
+// instructions per use.
+__host__ __device__ inline uint32_t div16_magic(uint32_t d) {
+  return d <= 1 ? 0u : uint32_t((uint64_t(1) << 32) / d + 1);
+}
+__device__ __forceinline__ uint32_t div16(uint32_t x, uint32_t m) {
+  const uint32_t q = __umulhi(x, m);
+  return m == 0 ? x : q;  // a select: a branch here splits the caller's code paths
+}
+
 // Load one element of a runtime-typed integer tensor as int64.
 __device__ __forceinline__ int64_t load_index(const void *p, int64_t i, int dt) {
   return dt == GDN_DT_I64 ? static_cast<const int64_t *>(p)[i] : int64_t(static_cast<const int32_t *>(p)[i]);
+}
+
+// load_index through the constant address space, for tables no kernel writes
+// while it reads them (block tables): at a uniform address it becomes a scalar
+// load, counted apart from the vector loads in flight. Read as a global
+// pointer inside a kernel that also stores, it becomes a vector load, and
+// waiting for it waits for every vector load issued before it.
+__device__ __forceinline__ int64_t load_index_ro(const void *p, int64_t i, int dt) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  if (dt == GDN_DT_I64) return reinterpret_cast<const __attribute__((address_space(4))) int64_t *>(a)[i];
+  return int64_t(reinterpret_cast<const __attribute__((address_space(4))) int32_t *>(a)[i]);
 }
 
 __device__ __forceinline__ void store_from_f32(void *p, int64_t i, int dt, float x) {

@@ -209,8 +209,8 @@ __device__ __forceinline__ void plan_finish_from(const PlanArgs &a, const gdn_pl
 
 __device__ __forceinline__ void plan_finish(const PlanArgs &a, const gdn_plan_group &g, PlanRow &r) {
   const PlanTable t = plan_table(a, g, r);
-  const int64_t fin = t.active ? load_index(g.block_table, t.final_el, g.table_dtype) : 0;
-  const int64_t bnd = t.load_b ? load_index(g.block_table, t.boundary_el, g.table_dtype) : 0;
+  const int64_t fin = t.active ? load_index_ro(g.block_table, t.final_el, g.table_dtype) : 0;
+  const int64_t bnd = t.load_b ? load_index_ro(g.block_table, t.boundary_el, g.table_dtype) : 0;
   plan_finish_from(a, g, r, t, fin, bnd);
 }
 
