@@ -206,4 +206,8 @@ __device__ __forceinline__ float dpp_sum8(float x) {
 // Thread-local error message set by the host entry points.
 void set_error(const char *fmt, ...);
 
+// Bytes of state a verify launch reads with ordinary loads, from the end of
+// its batch (gdn_recoverssm_set_state_cache_retain).
+int64_t state_cache_retain();
+
 }  // namespace gdn

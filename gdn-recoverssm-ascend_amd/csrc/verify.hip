@@ -209,6 +209,14 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     set_error("verify: grid too large");
     return GDN_ERR_UNSUPPORTED;
   }
+  // Rows read with ordinary loads: enough of the last rows to cover the
+  // retained bytes; the rows before them read their pages non-temporally.
+  {
+    const int64_t row_state = value_heads * V * state_vs * (E == 4 ? 4 : 2);
+    const int64_t keep = state_cache_retain();
+    const int64_t keep_rows = row_state <= 0 ? rows : keep / row_state + (keep % row_state != 0);
+    a.nt_rows = int32_t(rows > keep_rows ? rows - keep_rows : 0);
+  }
   auto s = static_cast<hipStream_t>(stream);
   const dim3 gd(static_cast<unsigned>(a.NVT * value_heads), static_cast<unsigned>(rows), 1u);
   switch (ext->state_dtype) {

@@ -72,6 +72,7 @@ struct VerifyArgs {
   int32_t p_corr_rs, p_key_rs, p_decay_rs;
   int32_t p_corr_hs, p_corr_ts, p_key_hs, p_key_ts, p_decay_hs, p_decay_ts;
   int32_t p_key_f32, p_key_per_value_head, p_record_rows, p_num_rows;
+  int32_t nt_rows;  // rows b < nt_rows read their state non-temporally
 };
 
 #ifndef GDN_V_STORE_END
@@ -91,6 +92,10 @@ constexpr int kTileRows = 128;     // eight MFMA row blocks of 16 rows
 // waves the launch's tail is shorter (measured: 232 against 236 us per step;
 // the plain verify is 3 us faster with whole tiles).
 constexpr int kDeferTileRows = 64;
+// One 16-row block of the state tile on its way from the row-contiguous load
+// layout to the matrix-core operand layout: 16 rows x 4J chunks of 16 bytes.
+__host__ __device__ constexpr int verify_stage_bytes(int j) { return 16 * 4 * j * 16; }
+extern __shared__ __align__(16) uint32_t verify_stage[][4];
 __host__ __device__ constexpr int verify_tile_rows(bool deferred) { return deferred ? kDeferTileRows : kTileRows; }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -114,6 +119,7 @@ __device__ __forceinline__ void st_f32_or(void *p, int64_t i, bool f32, float x)
 // Resources start at the wave's first token, so every in-bounds offset is far
 // below kWindowBytes (the host checks window extents against it).
 constexpr int kOutOfRange = 0x7ffff000;
+constexpr int kPolicyNT = 2;  // buffer cache policy bit: non-temporal
 constexpr int kWindowBytes = 0x7fff0000;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t byte_off) {
@@ -204,19 +210,31 @@ __device__ __forceinline__ void wave_lds_sync() {
 // final page (and the boundary snapshot to the boundary page), and the window
 // is verified from the folded values, rounded to the state type exactly as
 // the stored page is. Each state page is read once per step instead of twice.
-template <typename S, typename A, int J, int QM, bool DEFER>
-__global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
+// The wave's LDS, declared once per kernel and shared by both cache-policy
+// bodies below (a __shared__ array inside each would be allocated twice).
+// The non-temporal body also stages state blocks in dynamic LDS
+// (verify_stage_bytes), given to the launch only when it has such rows.
+template <int QM, int KP, int J, bool DEFER>
+struct VerifyLds {
+  float m[2 * QM][KP + 4];  // k and q~ vectors, row pitch KP + 4 (bank spread)
+  float gram[QM][2 * QM];
+  float d[64][2 * QM + 1];  // GEMV results of one 64-row half tile
+  float inv[2 * QM];
+  __align__(16) float pk[DEFER ? QM : 1][DEFER ? KP : 1];  // pending commit's keys
+};
+
+template <typename S, typename A, int J, int QM, bool DEFER, bool NT>
+__device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4 * Chunk<S>::E * J, J, DEFER> &L) {
   constexpr int E = Chunk<S>::E;       // elements per 16-byte chunk
   constexpr int KP = 4 * E * J;        // K padded to 4 k-slots x J chunks x E
   constexpr int NV = 2 * QM;           // used MFMA columns (<= 16)
-  constexpr int MP = KP + 4;           // LDS row pitch of the k/q vectors (bank spread)
   constexpr int TILE = verify_tile_rows(DEFER);
   constexpr int NRB = TILE / 16;  // 16-row MFMA blocks per tile (8 or 4)
-  __shared__ float m_lds[NV][MP];
-  __shared__ float gram_lds[QM][NV];
-  __shared__ float d_lds[64][NV + 1];  // GEMV results of one 64-row half tile
-  __shared__ float inv_lds[NV];
-  __shared__ __align__(16) float pk_lds[DEFER ? QM : 1][DEFER ? KP : 1];  // pending commit's keys
+  auto &m_lds = L.m;
+  auto &gram_lds = L.gram;
+  auto &d_lds = L.d;
+  auto &inv_lds = L.inv;
+  auto &pk_lds = L.pk;
 
   const int nvt = a.NVT;
   const int hv = int(blockIdx.x) / nvt;
@@ -414,10 +432,19 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   load_v(0);
 
   // ---- 3. first two state blocks ----
-  // Buffer loads: one resource per (slot, head) tile, a 32-bit per-lane offset
-  // per chunk and the block step in soffset. Rows >= V lie past the resource's
-  // extent and read as zero; chunks >= K get an out-of-range offset.
-  // Rows of block rb: rb*16 + li; the lane loads chunks 4j + ls of its row.
+  // Buffer loads: one resource per (slot, head) tile and a 32-bit per-lane
+  // offset per chunk. Rows >= V lie past the resource's extent and read as
+  // zero; chunks >= K get an out-of-range offset.
+  // Ordinary loads (NT false) read the operand layout directly: load j of
+  // block rb gives lane (li, ls) chunk 4j + ls of row rb*16 + li, 16 rows x
+  // 64 bytes per load. Non-temporal loads that touch half of each of 16 lines
+  // fetched lines twice and ran slower than ordinary ones (131 against 116 us
+  // for the B=256 tiles alone), so the non-temporal body (NT) reads whole
+  // rows: a block is 16 rows x CPR 16-byte chunks (CPR = 4J, the padded row),
+  // and its load j gives lane l the chunk (row j*RPL + l/CPR, chunk l%CPR),
+  // 1 KiB of consecutive bytes per load at K = 128 FP32 (102 us for the same
+  // tiles). The block then goes through LDS into the operand layout
+  // (`transpose` below); with ordinary loads that detour cost 4 us.
   const int tile_rows = V - row0 < TILE ? V - row0 : TILE;
   const int tile_bytes = tile_rows * a.state_vs * int(sizeof(S));
   auto tile_rsrc = [&](int64_t page, bool use) {
@@ -436,6 +463,12 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   // here became a 64-bit multiply-add whose unused high addend was a register
   // with a load in flight, and waiting for it held back the first state loads.
   const int lane_off = int(__umul24(unsigned(li), unsigned(row_bytes))) + ls * 16;
+  constexpr int CPR = 4 * J;     // 16-byte chunks per padded row (J <= 16)
+  constexpr int RPL = 64 / CPR;  // rows per load
+  const int c_chunk = lane & (CPR - 1), c_row = lane / CPR;
+  const bool c_ok = c_chunk * E < K;
+  const int c_off = int(__umul24(unsigned(c_row), unsigned(row_bytes))) + c_chunk * 16;
+  const int load_step = RPL * row_bytes;
   // The pending corrections of the lane's row, fetched with each block.
   const __amdgpu_buffer_rsrc_t rpc =
       make_rsrc(a.p_corr, (int64_t(prow) * a.p_corr_rs + int64_t(hv) * a.p_corr_hs + row0) * 4);
@@ -444,10 +477,17 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   // and the wait counts of every later MFMA would have to assume that path,
   // draining the pipeline at each block.
   auto load_block = [&](int rb, uint4 (&dst)[J], float (&pc)[QM]) {
+    // The block step rides in soffset, which the range check covers as well.
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
-      dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
+      if constexpr (NT) {
+        const int vo = c_ok ? c_off : kOutOfRange;
+        dst[j] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes + j * load_step, kPolicyNT));
+      } else {
+        const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
+        dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
+      }
     }
     if constexpr (DEFER) {
       const int v = rb * 16 + li;
@@ -459,6 +499,27 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
       for (int t = 0; t < QM; ++t)
         pc[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
             rpc, t < lim ? (t * a.p_corr_ts + v) * 4 : kOutOfRange, 0, 0));
+    }
+  };
+  // Row-contiguous block -> operand layout through LDS. Chunk c of block row
+  // r sits at r*CPR + (c ^ swz(r)): the 64 lanes of a write cover 64
+  // consecutive slots, and the 16 lanes (li = 0..15) of a read that share ls
+  // hit 16 distinct 16-byte bank groups.
+  constexpr int SWZ_MASK = (CPR < 16 ? CPR : 16) - 1;
+  constexpr int SWZ_SH = CPR >= 16 ? 0 : CPR == 8 ? 1 : 2;
+  auto swz = [](int r) { return (r >> SWZ_SH) & SWZ_MASK; };
+  auto transpose = [&](uint4 (&buf)[J]) {
+    if constexpr (NT) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int r = j * RPL + c_row;
+        *reinterpret_cast<uint4 *>(verify_stage[r * CPR + (c_chunk ^ swz(r))]) = buf[j];
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        buf[j] = *reinterpret_cast<const uint4 *>(verify_stage[li * CPR + ((4 * j + ls) ^ swz(li))]);
+      wave_lds_sync();  // the next block's writes stay behind these reads
     }
   };
   uint4 bufA[J], bufB[J];
@@ -720,9 +781,11 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   };
 #pragma unroll
   for (int rb = 0; rb < NRB; rb += 2) {
+    transpose(bufA);
     fold_block(rb, bufA, pcA);
     gemv_block(rb, bufA);
     if (rb + 2 < NRB) load_block(rb + 2, bufA, pcA);
+    transpose(bufB);
     fold_block(rb + 1, bufB, pcB);
     gemv_block(rb + 1, bufB);
     if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
@@ -737,17 +800,36 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   }
 }
 
+// Rows b < a.nt_rows read their state tiles with non-temporal loads, the
+// rest with ordinary ones. A launch streams its tiles once; what an ordinary
+// load leaves in the memory-side cache is what a commit reading the same pages
+// right after finds there, and only the last-read part of a large batch can
+// still be there. Reading the earlier part non-temporally keeps it from
+// evicting that part (and the non-temporal reads run faster): the host sets
+// nt_rows so that the ordinary reads cover the last `retain` bytes.
+template <typename S, typename A, int J, int QM, bool DEFER>
+__global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
+  __shared__ VerifyLds<QM, 4 * Chunk<S>::E * J, J, DEFER> lds;
+  if (int(blockIdx.y) < a.nt_rows)
+    verify_wave<S, A, J, QM, DEFER, true>(a, lds);
+  else
+    verify_wave<S, A, J, QM, DEFER, false>(a, lds);
+}
+
 // Launch for one state type; defined per state type in verify_<state>.hip.
 template <typename S>
 void launch_verify_state(int act_dt, int j, int qm, bool deferred, dim3 grid, hipStream_t s, const VerifyArgs &a);
 
 template <typename S, typename A, int J, bool DEFER>
 static void launch_verify_q(int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
+  // The staging block only for launches with non-temporal rows (it costs
+  // occupancy otherwise).
+  const unsigned lds = a.nt_rows > 0 ? unsigned(verify_stage_bytes(J)) : 0u;
   switch (qm) {
-    case 1: hipLaunchKernelGGL((verify_kernel<S, A, J, 1, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((verify_kernel<S, A, J, 2, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((verify_kernel<S, A, J, 4, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL((verify_kernel<S, A, J, 8, DEFER>), grid, dim3(kVerifyThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((verify_kernel<S, A, J, 1, DEFER>), grid, dim3(kVerifyThreads), lds, s, a); break;
+    case 2: hipLaunchKernelGGL((verify_kernel<S, A, J, 2, DEFER>), grid, dim3(kVerifyThreads), lds, s, a); break;
+    case 4: hipLaunchKernelGGL((verify_kernel<S, A, J, 4, DEFER>), grid, dim3(kVerifyThreads), lds, s, a); break;
+    default: hipLaunchKernelGGL((verify_kernel<S, A, J, 8, DEFER>), grid, dim3(kVerifyThreads), lds, s, a); break;
   }
 }
 

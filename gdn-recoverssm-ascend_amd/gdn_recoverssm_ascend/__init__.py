@@ -36,6 +36,22 @@ def initialize():
     return _native.load()
 
 
+def set_state_cache_retain(nbytes: int) -> int:
+    """Cache hint of this implementation (the reference has none): how many
+    bytes of checkpoint state each verify launch reads with ordinary loads,
+    counted from the end of its batch; earlier rows read their pages
+    non-temporally. Keep the default (256 MiB, the MI355X memory-side cache)
+    when a layer's commit directly follows its verify; set 0 when other
+    layers' verifies run in between (the model's decode step) or with the
+    deferred commit. Results are identical either way. Process-wide; returns
+    the previous value."""
+    from . import _native
+
+    if int(nbytes) < 0:
+        raise ValueError("GDN RecoverSSM: the retained state bytes must be >= 0")
+    return int(_native.load().gdn_recoverssm_set_state_cache_retain(int(nbytes)))
+
+
 __all__ = [
     "CommitEntry",
     "GDNRecoverSSMCommitContext",
@@ -54,4 +70,5 @@ __all__ = [
     "prepare_grouped_commit",
     "record_geometry_bytes",
     "record_nbytes",
+    "set_state_cache_retain",
 ]

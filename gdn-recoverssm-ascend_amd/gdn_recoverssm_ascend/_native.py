@@ -218,6 +218,8 @@ def load() -> ctypes.CDLL:
         lib.gdn_recoverssm_publish.argtypes = [
             c_vp, c_i64, c_vp, c_i32, c_i64, c_i64, c_vp, c_i32, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp,
         ]
+        lib.gdn_recoverssm_set_state_cache_retain.restype = c_i64
+        lib.gdn_recoverssm_set_state_cache_retain.argtypes = [c_i64]
         version = lib.gdn_recoverssm_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"GDN RecoverSSM HIP library ABI mismatch: {version} != {ABI_VERSION}")
@@ -256,6 +258,7 @@ def exported_symbols() -> tuple[str, ...]:
         "gdn_recoverssm_plan",
         "gdn_recoverssm_conv_compact",
         "gdn_recoverssm_publish",
+        "gdn_recoverssm_set_state_cache_retain",
     )
 
 

@@ -176,6 +176,22 @@ int gdn_recoverssm_verify_deferred(const void *q, const void *k, const void *v, 
                                    int64_t config_len, float scale, const gdn_verify_ext *ext,
                                    const gdn_pending_commit *pending, void *stream);
 
+/* Default of gdn_recoverssm_set_state_cache_retain: 256 MiB, the MI355X's
+ * memory-side (Infinity) cache. */
+#define GDN_STATE_CACHE_RETAIN_DEFAULT (256LL << 20)
+
+/* No counterpart in the reference (a cache hint of this implementation).
+ * How many bytes of checkpoint state a verify launch (any of the three entry
+ * points above) reads with ordinary loads, counted from the end of its batch:
+ * the rows before them read their pages non-temporally. A commit that reads
+ * the same pages right after the verify (verify, sampling, commit of one
+ * layer) finds the last-read part in the memory-side cache; set 0 when other
+ * layers' verifies run between a layer's verify and its commit (the model's
+ * decode step) or with the deferred commit, where nothing re-reads them soon.
+ * Results do not depend on it. Process-wide; returns the previous value, or
+ * -1 (nothing changed) for a negative `bytes`. */
+int64_t gdn_recoverssm_set_state_cache_retain(int64_t bytes);
+
 /* Grouped fold of the accepted prefix into every layer's checkpoint
  * (grouped_commit.py:377-480; csrc/fold.h:192-237). All table arguments are
  * DEVICE pointers: per-layer int64 base addresses / block strides [layers],

@@ -11,6 +11,8 @@ Tolerances (the bar for this path):
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 import gdn_oracle as O
@@ -44,3 +46,22 @@ def assert_state_close(got: torch.Tensor, want: torch.Tensor, what: str = "state
 def assert_norm_close(got: torch.Tensor, want: torch.Tensor, tol: float, what: str):
     err = O.rel_err_norm(got, want)
     assert err <= tol, f"{what}: norm-wise relative error {err:.3g} > {tol}"
+
+
+@contextlib.contextmanager
+def state_cache_retain(nbytes: int):
+    """Verify launches inside read all but the last `nbytes` of their state
+    non-temporally (gdn_recoverssm_set_state_cache_retain); restored after."""
+    import gdn_recoverssm_ascend as G
+
+    prev = G.set_state_cache_retain(nbytes)
+    try:
+        yield
+    finally:
+        G.set_state_cache_retain(prev)
+
+
+def retain_settings(rows: int, row_state_bytes: int) -> tuple[int, ...]:
+    """Settings that run a verify's state loads through each body: every row
+    non-temporal (0), the later half ordinary, every row ordinary."""
+    return (0, (rows // 2) * row_state_bytes, 1 << 50)

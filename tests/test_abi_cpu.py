@@ -43,6 +43,24 @@ def test_abi_version_and_error_channel():
     assert isinstance(lib.gdn_recoverssm_last_error(), bytes)
 
 
+def test_state_cache_retain_setting():
+    """The verify cache hint: default 256 MiB, returns the previous value,
+    rejects a negative byte count without changing the setting."""
+    import gdn_recoverssm_ascend as G
+
+    lib = N.load()
+    prev = lib.gdn_recoverssm_set_state_cache_retain(0)
+    try:
+        assert prev == 256 << 20
+        assert lib.gdn_recoverssm_set_state_cache_retain(-5) == -1
+        assert G.set_state_cache_retain(12345) == 0
+        with pytest.raises(ValueError, match="GDN RecoverSSM"):
+            G.set_state_cache_retain(-1)
+        assert G.set_state_cache_retain(prev) == 12345
+    finally:
+        lib.gdn_recoverssm_set_state_cache_retain(prev)
+
+
 def test_invalid_arguments_are_rejected_before_any_launch():
     lib = N.load()
     ext = N.VerifyExt(key_dim=128, value_dim=128)

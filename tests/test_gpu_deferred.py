@@ -34,7 +34,8 @@ from gdn_recoverssm_ascend.kernels import (
     gdn_recoverssm_verify,
     gdn_recoverssm_verify_deferred,
 )
-from gpu_helpers import CORR_TOL, OUT_TOL, assert_norm_close, assert_state_close
+from gpu_helpers import (CORR_TOL, OUT_TOL, assert_norm_close, assert_state_close, retain_settings,
+                         state_cache_retain)
 
 pytestmark = pytest.mark.gpu
 
@@ -300,6 +301,11 @@ def test_deferred_commit_equals_ordinary_flow(dev, seed, empty_row):
     got = _flow(w, dev, acc_steps, qsl_steps, deferred=True)
     _assert_flows_equal(ref, got)
     assert sum(int((h["plan"][2] > 0).sum()) for h in ref[0]) > 0
+    # Both state-load bodies of the verify: every row non-temporal, then the
+    # later half ordinary.
+    for retain in retain_settings(s.rows, s.value_heads * s.value_dim * s.key_dim * 4)[:2]:
+        with state_cache_retain(retain):
+            _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
 
 
 @pytest.mark.parametrize("K,V,Q,H,HV,act,state", [
@@ -325,8 +331,10 @@ def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act, s
     gen = torch.Generator().manual_seed(K * V + Q)
     acc_steps = [W.sample_accepted(s, s.rows, gen) for _ in range(steps)]
     qsl_steps = [w.meta.query_start_loc.clone() for _ in range(steps)]
-    _assert_flows_equal(_flow(w, dev, acc_steps, qsl_steps, deferred=False),
-                        _flow(w, dev, acc_steps, qsl_steps, deferred=True))
+    ref = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
+    _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
+    with state_cache_retain(0):  # every row's state read non-temporally
+        _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
 
 
 def _first_step(w, dev, acc):

@@ -12,7 +12,7 @@ import gdn_oracle as O
 from gdn_recoverssm_ascend import workloads as W
 from gdn_recoverssm_ascend.kernels import ReplayRecordBuffers, gdn_recoverssm_verify
 import sweep_cases as SC
-from gpu_helpers import CORR_TOL, OUT_TOL, assert_norm_close
+from gpu_helpers import CORR_TOL, OUT_TOL, assert_norm_close, retain_settings, state_cache_retain
 
 pytestmark = pytest.mark.gpu
 
@@ -56,23 +56,37 @@ def _run_and_check(P, dev, *, key_dtype=None, record_rows=None, packed=False, l2
         idx = table[:, 0]
     else:
         idx = P["idx"].to(idx_dtype).to(dev)
-    if packed:
-        rec = torch.full((R, HV, Q, V + K + 1), SENT, dtype=torch.float32, device=dev)
-    else:
-        rec = ReplayRecordBuffers(
-            torch.full((R, HV, Q, V), SENT, dtype=torch.float32, device=dev),
-            torch.full((R, H, Q, K), SENT, dtype=key_dtype, device=dev),
-            torch.full((R, HV, Q), SENT, dtype=torch.float32, device=dev),
+    def launch():
+        if packed:
+            rec = torch.full((R, HV, Q, V + K + 1), SENT, dtype=torch.float32, device=dev)
+        else:
+            rec = ReplayRecordBuffers(
+                torch.full((R, HV, Q, V), SENT, dtype=torch.float32, device=dev),
+                torch.full((R, H, Q, K), SENT, dtype=key_dtype, device=dev),
+                torch.full((R, HV, Q), SENT, dtype=torch.float32, device=dev),
+            )
+        out = torch.full((1, T, HV, V), SENT, dtype=out_dtype or v.dtype, device=dev)
+        ret = gdn_recoverssm_verify(
+            g, beta, q, k, v, checkpoint_state=ckpt, replay_cache=rec, query_start_loc=qsl, state_indices=idx,
+            spec_query_len=Q, qk_already_normalized=not l2norm, out=out, scale=scale,
         )
-    out = torch.full((1, T, HV, V), SENT, dtype=out_dtype or v.dtype, device=dev)
+        torch.cuda.synchronize()
+        assert ret is out
+        planes = (rec,) if packed else (rec.correction, rec.key, rec.decay)
+        return out, rec, planes
+
     before = ckpt.clone()
-    ret = gdn_recoverssm_verify(
-        g, beta, q, k, v, checkpoint_state=ckpt, replay_cache=rec, query_start_loc=qsl, state_indices=idx,
-        spec_query_len=Q, qk_already_normalized=not l2norm, out=out, scale=scale,
-    )
-    torch.cuda.synchronize()
-    assert ret is out
+    out, rec, planes = launch()
     assert torch.equal(ckpt, before), "verify must never write the checkpoint"
+    # The same launch with the state read non-temporally (whole-row loads
+    # turned into the operand layout through LDS) for every row, then for the
+    # earlier half: the same bits as the ordinary loads.
+    for retain in retain_settings(B, HV * V * K * ckpt.element_size())[:2]:
+        with state_cache_retain(retain):
+            out2, _, planes2 = launch()
+        assert torch.equal(out2, out), f"outputs differ with {retain} retained state bytes"
+        for a_, b_ in zip(planes2, planes):
+            assert torch.equal(a_, b_), f"records differ with {retain} retained state bytes"
     res = O.oracle_verify(
         inp.q, inp.k, inp.v, inp.g, inp.beta.to(beta_dtype), P["ckpt"], P["qsl"], P["idx"], Q, scale=scale,
         qk_already_normalized=not l2norm, record_rows=R, packed_key_per_value_head=packed,
@@ -195,6 +209,21 @@ def test_baseline_workloads(dev, name, rows):
                           query_start_loc=wd.meta.query_start_loc, state_indices=wd.meta.state_indices, spec_query_len=Q,
                           out=out)
     torch.cuda.synchronize()
+    # Every row non-temporal, and every row ordinary: the same bits as the
+    # default split.
+    for retain in retain_settings(B, HV * V * K * 4)[::2]:
+        rec2 = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=torch.bfloat16)
+        for t in (rec2.correction, rec2.key, rec2.decay):
+            t.fill_(SENT)
+        out2 = torch.full_like(out, SENT)
+        with state_cache_retain(retain):
+            gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=ckpt, replay_cache=rec2,
+                                  query_start_loc=wd.meta.query_start_loc, state_indices=wd.meta.state_indices,
+                                  spec_query_len=Q, out=out2)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out), f"{name}: outputs differ with {retain} retained state bytes"
+        for a_, b_ in zip((rec2.correction, rec2.key, rec2.decay), (rec.correction, rec.key, rec.decay)):
+            assert torch.equal(a_, b_), f"{name}: records differ with {retain} retained state bytes"
     sel = list(range(B)) if rows is None else sorted(torch.randperm(B, generator=torch.Generator().manual_seed(1))[:rows].tolist())
     if "padded_rows" in w.extras:
         sel = sorted(set(sel) | set(w.extras["padded_rows"].tolist()[:2]))
@@ -277,16 +306,25 @@ def _gated_check(dev, P, ab_dtype, param_dtype, seed=21):
     A_log = torch.randn(HV, generator=gen).to(param_dtype)
     dt_bias = torch.randn(HV, generator=gen).to(param_dtype)
     a[0, 0] = 30.0  # the linear branch of softplus
-    rec = ReplayRecordBuffers(
-        torch.full((B, HV, Q, V), SENT, device=dev), torch.full((B, H, Q, K), SENT, device=dev),
-        torch.full((B, HV, Q), SENT, device=dev),
-    )
-    out = torch.full((1, T, HV, V), SENT, dtype=inp.v.dtype, device=dev)
-    gdn_recoverssm_verify_gated(a.to(dev), b.to(dev), inp.q.to(dev), inp.k.to(dev), inp.v.to(dev),
-                                A_log=A_log.to(dev), dt_bias=dt_bias.to(dev), checkpoint_state=P["ckpt"].to(dev),
-                                replay_cache=rec, query_start_loc=P["qsl"].to(dev), state_indices=P["idx"].to(dev),
-                                spec_query_len=Q, out=out)
-    torch.cuda.synchronize()
+    def launch():
+        rec = ReplayRecordBuffers(
+            torch.full((B, HV, Q, V), SENT, device=dev), torch.full((B, H, Q, K), SENT, device=dev),
+            torch.full((B, HV, Q), SENT, device=dev),
+        )
+        out = torch.full((1, T, HV, V), SENT, dtype=inp.v.dtype, device=dev)
+        gdn_recoverssm_verify_gated(a.to(dev), b.to(dev), inp.q.to(dev), inp.k.to(dev), inp.v.to(dev),
+                                    A_log=A_log.to(dev), dt_bias=dt_bias.to(dev), checkpoint_state=P["ckpt"].to(dev),
+                                    replay_cache=rec, query_start_loc=P["qsl"].to(dev),
+                                    state_indices=P["idx"].to(dev), spec_query_len=Q, out=out)
+        torch.cuda.synchronize()
+        return out, rec
+
+    out, rec = launch()
+    with state_cache_retain(0):
+        out2, rec2 = launch()
+    assert torch.equal(out2, out)
+    for a_, b_ in zip((rec2.correction, rec2.key, rec2.decay), (rec.correction, rec.key, rec.decay)):
+        assert torch.equal(a_, b_), "gated records differ with the state read non-temporally"
     g, beta = O.oracle_gating(a, b, A_log, dt_bias)
     res = O.oracle_verify(inp.q, inp.k, inp.v, g, beta, P["ckpt"], P["qsl"], P["idx"], Q, qk_already_normalized=False)
     w = res.out_written
