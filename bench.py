@@ -176,7 +176,7 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
         return {"note": f"{_build.PROBE_LIB_PATH} not built"}
     lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
-    lib.gdn_probe_verify_twin.argtypes = [vp, vp, i64, vp, i64, vp, i64, vp, vp]
+    lib.gdn_probe_verify_twin.argtypes = [vp, vp, i64, vp, i64, vp, i64, vp, i64, vp]
     lib.gdn_probe_fold_twin.argtypes = [vp, vp, vp, vp, vp, i64, vp]
     s = w.spec
     B, HV, H, K, V = s.rows, s.value_heads, s.key_heads, s.key_dim, s.value_dim
@@ -187,10 +187,21 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     tile = V * K * 4
     page_b, head_b = ck.stride(0) * 4, ck.stride(1) * 4
     idx = w.meta.state_indices.cpu().long()
-    rows = idx[(idx > 0) & (idx < w.num_pages)]
+    valid = (idx > 0) & (idx < w.num_pages)
+    rows = idx[valid]
     hv = torch.arange(HV)
     tiles = (rows[:, None] * page_b + hv[None, :] * head_b).reshape(-1).to(dev)
     n_v = tiles.numel()
+    # The verify reads the rows before the last `retain` bytes of state
+    # non-temporally (whole rows) and the rest in the operand layout; the twin
+    # does the same for the same tiles.
+    from gdn_recoverssm_ascend import set_state_cache_retain
+
+    retain = set_state_cache_retain(0)
+    set_state_cache_retain(retain)
+    keep_rows = -(-retain // (HV * V * K * 4))
+    nt_rows = max(0, B - keep_rows)
+    nt_tiles = int(valid[:nt_rows].sum()) * HV
     T = nbytes["tokens"]
     writes = T * HV * V * (2 + 4) + T * H * K * 2 + T * HV * 4
     small = nbytes["verify"] - n_v * tile - writes
@@ -214,7 +225,7 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
 
     def vtwin(sdw=small_dw, wdw=write_dw):
         st = lib.gdn_probe_verify_twin(ck.data_ptr(), tiles.data_ptr(), n_v, small_buf.data_ptr(), sdw,
-                                       wbuf.data_ptr(), wdw, sink.data_ptr(), stream)
+                                       wbuf.data_ptr(), wdw, sink.data_ptr(), nt_tiles, stream)
         assert st == 0, f"verify twin: status {st}"
 
     def ftwin():
@@ -263,7 +274,8 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
         "note": "synthetic kernels moving the step's bytes in each kernel's access pattern with no arithmetic "
                 "(verify twin: the verify's state tiles, small reads and output / record writes; fold twin: the "
                 "committed tiles copied to their final and boundary pages of a scratch pool), timed as a step; "
-                "reads_only: the verify twin without its small reads and writes",
+                "reads_only: the verify twin without its small reads and writes; the verify twin reads the tiles "
+                "of the rows before the last retained bytes non-temporally, as the verify does",
     }
 
 
@@ -342,6 +354,68 @@ def other_configs(args, timer, skip):
         del w, rec, ctx, out, specs
         torch.cuda.empty_cache()
     return res
+
+
+def disjoint_pools(args, timer, name):
+    """The step on two batches of the workload with separate page pools (seeds
+    0 and 1) taking turns: no step finds the pages of the step before it in
+    any cache, so the only reuse left is the step's own (the commit reading
+    pages its verify has just read)."""
+    import torch
+
+    from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+
+    dev = torch.device("cuda:0")
+    keep, specs, total = [], [], 0
+    for seed in (0, 1):
+        w = W.make_workload(name, seed=seed, gen_device="cuda").to(dev)
+        s, m, inp = w.spec, w.meta, w.inputs[0]
+        B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+        align = m.block_table is not None
+        rec = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, [rec], spec_query_len=Q,
+                                                      max_num_reqs=B)
+        out = torch.empty(1, w.tokens, HV, V, dtype=inp.v.dtype, device=dev)
+        sp: list = []
+        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0], replay_cache=rec,
+                              query_start_loc=m.query_start_loc, state_indices=m.state_indices, spec_query_len=Q,
+                              out=out, _collect=sp)
+        sp += list(ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
+                                         block_table=m.block_table if align else None,
+                                         num_computed_tokens=m.num_computed if align else None,
+                                         mamba_block_size=m.block_size if align else None, commit_conv=False))
+        specs.append(sp)
+        keep.append((w, rec, ctx, out))
+
+    def two_steps():
+        for sp in specs[0] + specs[1]:
+            sp.launch()
+
+    for _ in range(max(1, args.warmup // 2)):
+        two_steps()
+    e0, e1 = timer.event(), timer.event()
+    torch.cuda.synchronize()
+    timer.record(e0)
+    for _ in range(max(1, args.steps // 2)):
+        two_steps()
+    timer.record(e1)
+    torch.cuda.synchronize()
+    pairs = max(1, args.steps // 2)
+    us = timer.elapsed(e0, e1) / (2 * pairs) * 1e3
+    # The plan arrays hold each batch's plan now that its commits have run.
+    for w, _, ctx, _ in keep:
+        nb = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices,
+                        ctx.boundary_recovery_lens)
+        total += nb["verify"] + nb["commit"]
+    bytes_per_step = total / 2
+    del keep, specs
+    torch.cuda.empty_cache()
+    return {"us_per_step": round(us, 2), "bytes_per_step": int(bytes_per_step),
+            "gbs": round(bytes_per_step / (us * 1e-6) / 1e9, 1),
+            "frac": round(bytes_per_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "the step on two batches with separate page pools taking turns (seeds 0 and 1): no step "
+                    "finds the previous step's pages in a cache; only the step's own verify -> commit reuse is left"}
 
 
 def cpu_baseline(w_cpu, threads, budget_s=10.0):
@@ -821,6 +895,7 @@ def main():
         plan4 = (ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices, ctx.boundary_recovery_lens)
         ceiling = traffic_ceiling(w, nbytes, plan4, {k: v * 1e3 for k, v in kernel_ms.items()}, timer, args.steps)
     others = None if args.kernel_only else other_configs(args, timer, s.name)
+    pools = None if args.kernel_only else disjoint_pools(args, timer, s.name)
     # The 48-layer decode loop at its own size (its own 10 warmup steps, after
     # which the carried state restarts from the seeded start).
     loop = None if args.kernel_only else decode_loop_summary(warmup=10)
@@ -957,6 +1032,7 @@ def main():
         "deferred_commit": deferred,
         "traffic_ceiling": ceiling,
         "other_configs": others,
+        "disjoint_pools": pools,
         "decode_loop": loop,
     }
     print(json.dumps(line), flush=True)

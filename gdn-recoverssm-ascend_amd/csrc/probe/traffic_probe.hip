@@ -23,29 +23,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *p, int b
 
 // The verify's traffic: one wave per tile; `small_dw` dwords read from a
 // region two consecutive waves share (q and k are shared by the two value
-// heads of a key head); the tile streamed as eight 16-row blocks in the
-// matrix-core operand layout (lane (r = l % 16, s = l / 16) reads the 16-byte
-// chunks 4j + s of row r), two blocks in flight; `write_dw` dwords written
-// per wave, half after each 64-row half tile, as the verify stores its
-// outputs and records.
-__global__ __launch_bounds__(64) void verify_twin(const char *__restrict__ state, const int64_t *__restrict__ tiles,
-                                                  const float *__restrict__ small, int small_dw,
-                                                  float *__restrict__ wbuf, int write_dw, float *__restrict__ sink) {
-  const int64_t w = blockIdx.x;
-  const int lane = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t r = tile_rsrc(state + tiles[w], kTileBytes);
-  float acc = 0.0f;
-  const float *sp = small + (w / 2) * int64_t(small_dw);
-  for (int i = lane; i < small_dw; i += 64) acc += sp[i];
+// heads of a key head); the tile streamed as eight 16-row blocks, two blocks
+// in flight; `write_dw` dwords written per wave, half after each 64-row half
+// tile, as the verify stores its outputs and records. Tiles w < nt_tiles read
+// whole rows with non-temporal loads (lane l, load j: bytes 16 l + 1024 j of
+// the block), the rest the matrix-core operand layout with ordinary loads
+// (lane (r = l % 16, s = l / 16) reads the 16-byte chunks 4j + s of row r),
+// as the verify's two bodies do.
+template <bool NT>
+__device__ __forceinline__ float verify_twin_tile(__amdgpu_buffer_rsrc_t r, __amdgpu_buffer_rsrc_t wr, int lane,
+                                                  int write_dw, float acc) {
+  constexpr int pol = NT ? kNT : 0;
   int voff[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) voff[j] = (lane & 15) * kRowBytes + (4 * j + (lane >> 4)) * 16;
+  for (int j = 0; j < 8; ++j) voff[j] = NT ? lane * 16 + j * 1024 : (lane & 15) * kRowBytes + (4 * j + (lane >> 4)) * 16;
   u32x4 a[8], b[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], 0, 0);
+  for (int j = 0; j < 8; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], 0, pol);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], 16 * kRowBytes, 0);
-  const __amdgpu_buffer_rsrc_t wr = tile_rsrc(reinterpret_cast<const char *>(wbuf + w * int64_t(write_dw)), write_dw * 4);
+  for (int j = 0; j < 8; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], 16 * kRowBytes, pol);
   const int per_half = write_dw / 2;
 #pragma unroll
   for (int blk = 0; blk < 8; blk += 2) {
@@ -53,13 +49,13 @@ __global__ __launch_bounds__(64) void verify_twin(const char *__restrict__ state
     for (int j = 0; j < 8; ++j) acc += __uint_as_float(a[j][0] ^ a[j][3]);
     if (blk + 2 < 8) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], (blk + 2) * 16 * kRowBytes, 0);
+      for (int j = 0; j < 8; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], (blk + 2) * 16 * kRowBytes, pol);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc += __uint_as_float(b[j][0] ^ b[j][3]);
     if (blk + 3 < 8) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], (blk + 3) * 16 * kRowBytes, 0);
+      for (int j = 0; j < 8; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], (blk + 3) * 16 * kRowBytes, pol);
     }
     if (blk == 2 || blk == 6) {
       const int base = blk == 2 ? 0 : per_half;
@@ -68,7 +64,27 @@ __global__ __launch_bounds__(64) void verify_twin(const char *__restrict__ state
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc + float(i)), wr, (base + i) * 4, 0, 0);
     }
   }
-  if (lane == 0) sink[w] = acc;
+  return acc;
+}
+
+__global__ __launch_bounds__(64) void verify_twin(const char *__restrict__ state, const int64_t *__restrict__ tiles,
+                                                  const float *__restrict__ small, int small_dw,
+                                                  float *__restrict__ wbuf, int write_dw, float *__restrict__ sink,
+                                                  int nt_tiles) {
+  const int64_t w = blockIdx.x;
+  const int lane = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t r = tile_rsrc(state + tiles[w], kTileBytes);
+  float acc = 0.0f;
+  const float *sp = small + (w / 2) * int64_t(small_dw);
+  for (int i = lane; i < small_dw; i += 64) acc += sp[i];
+  const __amdgpu_buffer_rsrc_t wr = tile_rsrc(reinterpret_cast<const char *>(wbuf + w * int64_t(write_dw)), write_dw * 4);
+  if (w < nt_tiles)
+    acc = verify_twin_tile<true>(r, wr, lane, write_dw, acc);
+  else
+    acc = verify_twin_tile<false>(r, wr, lane, write_dw, acc);
+  // Every lane's loads feed the stored value (a store by lane 0 alone would
+  // let the compiler drop the other lanes' loads); the test never holds.
+  if (__float_as_uint(acc) == 0x7f800001u) sink[w] = acc;
 }
 
 // The fold's traffic: one 256-thread workgroup per tile; each thread reads
@@ -102,12 +118,13 @@ __global__ __launch_bounds__(256) void fold_twin(const char *__restrict__ src, c
 // write_dw bytes fit a 32-bit buffer extent.
 extern "C" int gdn_probe_verify_twin(const void *state, const int64_t *tile_offsets, int64_t n_tiles,
                                      const float *small, int64_t small_dw, float *wbuf, int64_t write_dw,
-                                     float *sink, void *stream) {
+                                     float *sink, int64_t nt_tiles, void *stream) {
   if (!state || !tile_offsets || !sink || n_tiles <= 0 || n_tiles > 0x7fffffffLL || small_dw < 0 ||
       small_dw > (1 << 20) || write_dw < 0 || write_dw > (1 << 20) || (small_dw && !small) || (write_dw && !wbuf))
     return 1;
   hipLaunchKernelGGL(verify_twin, dim3(unsigned(n_tiles)), dim3(64), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const char *>(state), tile_offsets, small, int(small_dw), wbuf, int(write_dw), sink);
+                     static_cast<const char *>(state), tile_offsets, small, int(small_dw), wbuf, int(write_dw), sink,
+                     int(nt_tiles < 0 ? 0 : nt_tiles > n_tiles ? n_tiles : nt_tiles));
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

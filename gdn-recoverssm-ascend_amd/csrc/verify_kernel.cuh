@@ -24,9 +24,11 @@
 //
 // MFMA operand layout (16x16x4, wave64): A lane l = (row l%16, k-slot l/16),
 // B lane l = (k-slot l/16, column l%16), D lane l register r = (row
-// 4*(l/16)+r, column l%16). Lane (i, s) loads the 16-byte chunks 4j+s of its
+// 4*(l/16)+r, column l%16). Lane (i, s) holds the 16-byte chunks 4j+s of its
 // row, so the k-slot s of MFMA (j, e) holds element E*(4j+s)+e; B uses the
-// same permutation of K.
+// same permutation of K. Rows read with ordinary loads are loaded in that
+// layout; rows read non-temporally (the early rows of a large batch, see
+// verify_kernel) are loaded as whole rows and reach it through LDS.
 //
 // Template parameters: S state element type, A activation type (q, k, v and
 // the key record / output when they share it), J 16-byte chunks per lane per
@@ -508,17 +510,23 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
   constexpr int SWZ_MASK = (CPR < 16 ? CPR : 16) - 1;
   constexpr int SWZ_SH = CPR >= 16 ? 0 : CPR == 8 ? 1 : 2;
   auto swz = [](int r) { return (r >> SWZ_SH) & SWZ_MASK; };
+  auto stage_write = [&](const uint4 (&buf)[J]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int r = j * RPL + c_row;
+      *reinterpret_cast<uint4 *>(verify_stage[r * CPR + (c_chunk ^ swz(r))]) = buf[j];
+    }
+  };
+  auto stage_read = [&](uint4 (&buf)[J]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      buf[j] = *reinterpret_cast<const uint4 *>(verify_stage[li * CPR + ((4 * j + ls) ^ swz(li))]);
+  };
   auto transpose = [&](uint4 (&buf)[J]) {
     if constexpr (NT) {
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int r = j * RPL + c_row;
-        *reinterpret_cast<uint4 *>(verify_stage[r * CPR + (c_chunk ^ swz(r))]) = buf[j];
-      }
+      stage_write(buf);
       wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        buf[j] = *reinterpret_cast<const uint4 *>(verify_stage[li * CPR + ((4 * j + ls) ^ swz(li))]);
+      stage_read(buf);
       wave_lds_sync();  // the next block's writes stay behind these reads
     }
   };
@@ -781,14 +789,32 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
   };
 #pragma unroll
   for (int rb = 0; rb < NRB; rb += 2) {
-    transpose(bufA);
-    fold_block(rb, bufA, pcA);
-    gemv_block(rb, bufA);
-    if (rb + 2 < NRB) load_block(rb + 2, bufA, pcA);
-    transpose(bufB);
-    fold_block(rb + 1, bufB, pcB);
-    gemv_block(rb + 1, bufB);
-    if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
+    if constexpr (NT && !DEFER) {
+      // Once a block sits in LDS its registers take the block after next:
+      // those loads issue before the block's read-back and matrix work.
+      uint4 op[J];
+      stage_write(bufA);
+      if (rb + 2 < NRB) load_block(rb + 2, bufA, pcA);
+      wave_lds_sync();
+      stage_read(op);
+      wave_lds_sync();
+      gemv_block(rb, op);
+      stage_write(bufB);
+      if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
+      wave_lds_sync();
+      stage_read(op);
+      wave_lds_sync();
+      gemv_block(rb + 1, op);
+    } else {
+      transpose(bufA);
+      fold_block(rb, bufA, pcA);
+      gemv_block(rb, bufA);
+      if (rb + 2 < NRB) load_block(rb + 2, bufA, pcA);
+      transpose(bufB);
+      fold_block(rb + 1, bufB, pcB);
+      gemv_block(rb + 1, bufB);
+      if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
+    }
     if (NRB == 8 && rb + 2 == NRB / 2) load_v(1);  // a half tile has no second half
     // Every half runs its recurrence, also one past V (its rows store nothing):
     // skipping it would be a path without its stores.

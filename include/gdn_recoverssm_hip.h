@@ -25,6 +25,7 @@
  *   gdn_recoverssm_verify_deferred -> the "deferred commit" of docs/GDN-RecoverSSM-实现方案.md:515-527,
  *                                   563-568: the fold (csrc/ops.cpp:170-239) applied inside the
  *                                   next step's verify
+ *   gdn_recoverssm_set_state_cache_retain -> no counterpart: a cache hint for the verify launches
  */
 #ifndef GDN_RECOVERSSM_HIP_H
 #define GDN_RECOVERSSM_HIP_H
