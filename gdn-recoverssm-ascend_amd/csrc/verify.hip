@@ -211,7 +211,12 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
   }
   // Rows read with ordinary loads: enough of the last rows to cover the
   // retained bytes; the rows before them read their pages non-temporally.
-  {
+  // The deferred verify reads and writes every row non-temporally: the
+  // pages it folds are next read by the following step's verify, never
+  // right after.
+  if (pending) {
+    a.nt_rows = int32_t(rows);
+  } else {
     const int64_t row_state = value_heads * V * state_vs * (E == 4 ? 4 : 2);
     const int64_t keep = state_cache_retain();
     const int64_t keep_rows = row_state <= 0 ? rows : keep / row_state + (keep % row_state != 0);

@@ -648,12 +648,34 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
         }
       };
       auto store = [&](__amdgpu_buffer_rsrc_t r) {
+        if constexpr (NT) {
+          // Whole rows, non-temporal: the folded chunks go back through LDS
+          // into the load layout (each lane writes the slots it read its
+          // operands from). Stores of 64-byte pieces of 16 rows ran slower,
+          // and non-temporal ones much slower: a synthetic twin of this
+          // launch's traffic took 224 us with the operand-layout stores and
+          // 192 us with whole-row non-temporal ones.
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, pack16<S>(h[j])), r, vo,
-              rb * 16 * row_bytes, 0);
+          for (int j = 0; j < J; ++j)
+            *reinterpret_cast<uint4 *>(verify_stage[li * CPR + ((4 * j + ls) ^ swz(li))]) = pack16<S>(h[j]);
+          wave_lds_sync();
+#pragma unroll
+          for (int j = 0; j < J; ++j) {
+            const int rr = j * RPL + c_row;
+            const uint4 x = *reinterpret_cast<const uint4 *>(verify_stage[rr * CPR + (c_chunk ^ swz(rr))]);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, x),
+                                                   r, c_ok ? c_off : kOutOfRange,
+                                                   rb * 16 * row_bytes + j * load_step, kPolicyNT);
+          }
+          wave_lds_sync();
+        } else {
+#pragma unroll
+          for (int j = 0; j < J; ++j) {
+            const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, pack16<S>(h[j])), r, vo,
+                rb * 16 * row_bytes, 0);
+          }
         }
       };
       apply(0, seg);
@@ -836,7 +858,7 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
 template <typename S, typename A, int J, int QM, bool DEFER>
 __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
   __shared__ VerifyLds<QM, 4 * Chunk<S>::E * J, J, DEFER> lds;
-  if (int(blockIdx.y) < a.nt_rows)
+  if (DEFER || int(blockIdx.y) < a.nt_rows)  // the deferred verify: every row (see verify.hip)
     verify_wave<S, A, J, QM, DEFER, true>(a, lds);
   else
     verify_wave<S, A, J, QM, DEFER, false>(a, lds);
@@ -850,7 +872,7 @@ template <typename S, typename A, int J, bool DEFER>
 static void launch_verify_q(int qm, dim3 grid, hipStream_t s, const VerifyArgs &a) {
   // The staging block only for launches with non-temporal rows (it costs
   // occupancy otherwise).
-  const unsigned lds = a.nt_rows > 0 ? unsigned(verify_stage_bytes(J)) : 0u;
+  const unsigned lds = DEFER || a.nt_rows > 0 ? unsigned(verify_stage_bytes(J)) : 0u;
   switch (qm) {
     case 1: hipLaunchKernelGGL((verify_kernel<S, A, J, 1, DEFER>), grid, dim3(kVerifyThreads), lds, s, a); break;
     case 2: hipLaunchKernelGGL((verify_kernel<S, A, J, 2, DEFER>), grid, dim3(kVerifyThreads), lds, s, a); break;

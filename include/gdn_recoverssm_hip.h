@@ -182,15 +182,15 @@ int gdn_recoverssm_verify_deferred(const void *q, const void *k, const void *v, 
 #define GDN_STATE_CACHE_RETAIN_DEFAULT (256LL << 20)
 
 /* No counterpart in the reference (a cache hint of this implementation).
- * How many bytes of checkpoint state a verify launch (any of the three entry
- * points above) reads with ordinary loads, counted from the end of its batch:
- * the rows before them read their pages non-temporally. A commit that reads
- * the same pages right after the verify (verify, sampling, commit of one
- * layer) finds the last-read part in the memory-side cache; set 0 when other
- * layers' verifies run between a layer's verify and its commit (the model's
- * decode step) or with the deferred commit, where nothing re-reads them soon.
- * Results do not depend on it. Process-wide; returns the previous value, or
- * -1 (nothing changed) for a negative `bytes`. */
+ * How many bytes of checkpoint state a verify launch (gdn_recoverssm_verify,
+ * gdn_recoverssm_verify_gated) reads with ordinary loads, counted from the end
+ * of its batch: the rows before them read their pages non-temporally. A
+ * commit that reads the same pages right after the verify (verify, sampling,
+ * commit of one layer) finds the last-read part in the memory-side cache.
+ * gdn_recoverssm_verify_deferred reads and writes every row non-temporally
+ * whatever the setting (nothing re-reads its pages soon). Results do not
+ * depend on it. Process-wide; returns the previous value, or -1 (nothing
+ * changed) for a negative `bytes`. */
 int64_t gdn_recoverssm_set_state_cache_retain(int64_t bytes);
 
 /* Grouped fold of the accepted prefix into every layer's checkpoint
