@@ -96,7 +96,10 @@ constexpr int kTileRows = 128;     // eight MFMA row blocks of 16 rows
 constexpr int kDeferTileRows = 64;
 // One 16-row block of the state tile on its way from the row-contiguous load
 // layout to the matrix-core operand layout: 16 rows x 4J chunks of 16 bytes.
-__host__ __device__ constexpr int verify_stage_bytes(int j) { return 16 * 4 * j * 16; }
+// It is staged in two rounds of half the row's chunks (one for J = 1), so the
+// stage holds 16 rows x 2J chunks.
+__host__ __device__ constexpr int verify_stage_rounds(int j) { return j >= 2 ? 2 : 1; }
+__host__ __device__ constexpr int verify_stage_bytes(int j) { return 16 * (4 * j / verify_stage_rounds(j)) * 16; }
 extern __shared__ __align__(16) uint32_t verify_stage[][4];
 __host__ __device__ constexpr int verify_tile_rows(bool deferred) { return deferred ? kDeferTileRows : kTileRows; }
 
@@ -441,12 +444,15 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
   // block rb gives lane (li, ls) chunk 4j + ls of row rb*16 + li, 16 rows x
   // 64 bytes per load. Non-temporal loads that touch half of each of 16 lines
   // fetched lines twice and ran slower than ordinary ones (131 against 116 us
-  // for the B=256 tiles alone), so the non-temporal body (NT) reads whole
-  // rows: a block is 16 rows x CPR 16-byte chunks (CPR = 4J, the padded row),
-  // and its load j gives lane l the chunk (row j*RPL + l/CPR, chunk l%CPR),
-  // 1 KiB of consecutive bytes per load at K = 128 FP32 (102 us for the same
-  // tiles). The block then goes through LDS into the operand layout
-  // (`transpose` below); with ordinary loads that detour cost 4 us.
+  // for the B=256 tiles alone), so the non-temporal body (NT) reads rows in
+  // long runs: a block is 16 rows x CPR 16-byte chunks (CPR = 4J, the padded
+  // row), staged through LDS into the operand layout in ROUNDS rounds of SC =
+  // CPR / ROUNDS chunks per row (`transpose` below; with ordinary loads that
+  // detour cost 4 us). Load j belongs to round g = j / JR and gives lane l the
+  // chunk (row (j % JR)*RPL + l/SC, chunk g*SC + l%SC): 4 rows x 256 bytes per
+  // load at K = 128 FP32 (whole rows measured 102 us for the same tiles, runs
+  // of 256 bytes 104 us, and halving the stage keeps the LDS from limiting
+  // the waves per CU).
   const int tile_rows = V - row0 < TILE ? V - row0 : TILE;
   const int tile_bytes = tile_rows * a.state_vs * int(sizeof(S));
   auto tile_rsrc = [&](int64_t page, bool use) {
@@ -465,12 +471,18 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
   // here became a 64-bit multiply-add whose unused high addend was a register
   // with a load in flight, and waiting for it held back the first state loads.
   const int lane_off = int(__umul24(unsigned(li), unsigned(row_bytes))) + ls * 16;
-  constexpr int CPR = 4 * J;     // 16-byte chunks per padded row (J <= 16)
-  constexpr int RPL = 64 / CPR;  // rows per load
-  const int c_chunk = lane & (CPR - 1), c_row = lane / CPR;
-  const bool c_ok = c_chunk * E < K;
+  constexpr int CPR = 4 * J;                 // 16-byte chunks per padded row (J <= 16)
+  constexpr int ROUNDS = verify_stage_rounds(J);
+  constexpr int SC = CPR / ROUNDS;           // chunks of each row staged per round
+  constexpr int JR = J / ROUNDS;             // loads (and operand registers) per round
+  constexpr int RPL = 64 / SC;               // rows per load
+  const int c_chunk = lane & (SC - 1), c_row = lane / SC;
   const int c_off = int(__umul24(unsigned(c_row), unsigned(row_bytes))) + c_chunk * 16;
   const int load_step = RPL * row_bytes;
+  // Lane offset of load j (its round's chunks past K read and write nothing)
+  // and the uniform part that rides in soffset.
+  auto c_voff = [&](int j) { return ((j / JR) * SC + c_chunk) * E < K ? c_off : kOutOfRange; };
+  auto c_soff = [&](int rb, int j) { return rb * 16 * row_bytes + (j % JR) * load_step + (j / JR) * SC * 16; };
   // The pending corrections of the lane's row, fetched with each block.
   const __amdgpu_buffer_rsrc_t rpc =
       make_rsrc(a.p_corr, (int64_t(prow) * a.p_corr_rs + int64_t(hv) * a.p_corr_hs + row0) * 4);
@@ -483,9 +495,7 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       if constexpr (NT) {
-        const int vo = c_ok ? c_off : kOutOfRange;
-        dst[j] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes + j * load_step, kPolicyNT));
+        dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, c_voff(j), c_soff(rb, j), kPolicyNT));
       } else {
         const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
         dst[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo, rb * 16 * row_bytes, 0));
@@ -503,31 +513,36 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
             rpc, t < lim ? (t * a.p_corr_ts + v) * 4 : kOutOfRange, 0, 0));
     }
   };
-  // Row-contiguous block -> operand layout through LDS. Chunk c of block row
-  // r sits at r*CPR + (c ^ swz(r)): the 64 lanes of a write cover 64
-  // consecutive slots, and the 16 lanes (li = 0..15) of a read that share ls
-  // hit 16 distinct 16-byte bank groups.
-  constexpr int SWZ_MASK = (CPR < 16 ? CPR : 16) - 1;
-  constexpr int SWZ_SH = CPR >= 16 ? 0 : CPR == 8 ? 1 : 2;
+  // Row-run block -> operand layout through LDS, one round at a time. In a
+  // round, chunk c (of the round's SC) of block row r sits at r*SC +
+  // (c ^ swz(r)): the 64 lanes of a write cover 64 consecutive slots, and the
+  // 16 lanes (li = 0..15) of a read that share ls hit 16 distinct 16-byte
+  // bank groups. Operand register j (chunk 4j + ls) belongs to round j / JR.
+  constexpr int SWZ_MASK = (SC < 16 ? SC : 16) - 1;
+  constexpr int SWZ_SH = SC >= 16 ? 0 : SC == 8 ? 1 : 2;
   auto swz = [](int r) { return (r >> SWZ_SH) & SWZ_MASK; };
-  auto stage_write = [&](const uint4 (&buf)[J]) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int r = j * RPL + c_row;
-      *reinterpret_cast<uint4 *>(verify_stage[r * CPR + (c_chunk ^ swz(r))]) = buf[j];
-    }
+  auto row_slot = [&](int j) {  // slot of load j's chunk
+    const int r = (j % JR) * RPL + c_row;
+    return r * SC + (c_chunk ^ swz(r));
   };
-  auto stage_read = [&](uint4 (&buf)[J]) {
+  auto op_slot = [&](int j) { return li * SC + ((4 * (j % JR) + ls) ^ swz(li)); };  // slot of operand register j
+  auto stage_write = [&](const uint4 (&buf)[J], int g) {
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-      buf[j] = *reinterpret_cast<const uint4 *>(verify_stage[li * CPR + ((4 * j + ls) ^ swz(li))]);
+    for (int j = g * JR; j < (g + 1) * JR; ++j) *reinterpret_cast<uint4 *>(verify_stage[row_slot(j)]) = buf[j];
+  };
+  auto stage_read = [&](uint4 (&buf)[J], int g) {
+#pragma unroll
+    for (int j = g * JR; j < (g + 1) * JR; ++j) buf[j] = *reinterpret_cast<const uint4 *>(verify_stage[op_slot(j)]);
   };
   auto transpose = [&](uint4 (&buf)[J]) {
     if constexpr (NT) {
-      stage_write(buf);
-      wave_lds_sync();
-      stage_read(buf);
-      wave_lds_sync();  // the next block's writes stay behind these reads
+#pragma unroll
+      for (int g = 0; g < ROUNDS; ++g) {
+        stage_write(buf, g);
+        wave_lds_sync();
+        stage_read(buf, g);
+        wave_lds_sync();  // the next round's writes stay behind these reads
+      }
     }
   };
   uint4 bufA[J], bufB[J];
@@ -656,18 +671,20 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
           // launch's traffic took 224 us with the operand-layout stores and
           // 192 us with whole-row non-temporal ones.
 #pragma unroll
-          for (int j = 0; j < J; ++j)
-            *reinterpret_cast<uint4 *>(verify_stage[li * CPR + ((4 * j + ls) ^ swz(li))]) = pack16<S>(h[j]);
-          wave_lds_sync();
+          for (int g = 0; g < ROUNDS; ++g) {
 #pragma unroll
-          for (int j = 0; j < J; ++j) {
-            const int rr = j * RPL + c_row;
-            const uint4 x = *reinterpret_cast<const uint4 *>(verify_stage[rr * CPR + (c_chunk ^ swz(rr))]);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, x),
-                                                   r, c_ok ? c_off : kOutOfRange,
-                                                   rb * 16 * row_bytes + j * load_step, kPolicyNT);
+            for (int j = g * JR; j < (g + 1) * JR; ++j)
+              *reinterpret_cast<uint4 *>(verify_stage[op_slot(j)]) = pack16<S>(h[j]);
+            wave_lds_sync();
+#pragma unroll
+            for (int j = g * JR; j < (g + 1) * JR; ++j) {
+              const uint4 x = *reinterpret_cast<const uint4 *>(verify_stage[row_slot(j)]);
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, x), r, c_voff(j), c_soff(rb, j),
+                  kPolicyNT);
+            }
+            wave_lds_sync();
           }
-          wave_lds_sync();
         } else {
 #pragma unroll
           for (int j = 0; j < J; ++j) {
@@ -813,19 +830,22 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
   for (int rb = 0; rb < NRB; rb += 2) {
     if constexpr (NT && !DEFER) {
       // Once a block sits in LDS its registers take the block after next:
-      // those loads issue before the block's read-back and matrix work.
+      // those loads issue before the block's last read-back and its matrix
+      // work.
       uint4 op[J];
-      stage_write(bufA);
-      if (rb + 2 < NRB) load_block(rb + 2, bufA, pcA);
-      wave_lds_sync();
-      stage_read(op);
-      wave_lds_sync();
+      auto stage_block = [&](int next, uint4 (&buf)[J], float (&pc)[QM]) {
+#pragma unroll
+        for (int g = 0; g < ROUNDS; ++g) {
+          stage_write(buf, g);
+          if (g + 1 == ROUNDS && next < NRB) load_block(next, buf, pc);
+          wave_lds_sync();
+          stage_read(op, g);
+          wave_lds_sync();
+        }
+      };
+      stage_block(rb + 2, bufA, pcA);
       gemv_block(rb, op);
-      stage_write(bufB);
-      if (rb + 3 < NRB) load_block(rb + 3, bufB, pcB);
-      wave_lds_sync();
-      stage_read(op);
-      wave_lds_sync();
+      stage_block(rb + 3, bufB, pcB);
       gemv_block(rb + 1, op);
     } else {
       transpose(bufA);
