@@ -193,7 +193,7 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     tiles = (rows[:, None] * page_b + hv[None, :] * head_b).reshape(-1).to(dev)
     n_v = tiles.numel()
     # The verify reads the rows before the last `retain` bytes of state
-    # non-temporally (whole rows) and the rest in the operand layout; the twin
+    # non-temporally (row runs) and the rest in the operand layout; the twin
     # does the same for the same tiles.
     from gdn_recoverssm_ascend import set_state_cache_retain
 
@@ -275,7 +275,7 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
                 "(verify twin: the verify's state tiles, small reads and output / record writes; fold twin: the "
                 "committed tiles copied to their final and boundary pages of a scratch pool), timed as a step; "
                 "reads_only: the verify twin without its small reads and writes; the verify twin reads the tiles "
-                "of the rows before the last retained bytes non-temporally, as the verify does",
+                "of the rows before the last retained bytes non-temporally in row runs, as the verify does",
     }
 
 

@@ -26,17 +26,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *p, int b
 // heads of a key head); the tile streamed as eight 16-row blocks, two blocks
 // in flight; `write_dw` dwords written per wave, half after each 64-row half
 // tile, as the verify stores its outputs and records. Tiles w < nt_tiles read
-// whole rows with non-temporal loads (lane l, load j: bytes 16 l + 1024 j of
-// the block), the rest the matrix-core operand layout with ordinary loads
-// (lane (r = l % 16, s = l / 16) reads the 16-byte chunks 4j + s of row r),
-// as the verify's two bodies do.
+// row runs with non-temporal loads (lane l, load j: row 4 (j % 4) + l / 16,
+// 16-byte chunk 16 (j / 4) + l % 16 of the block: 4 rows x 256 bytes), the
+// rest the matrix-core operand layout with ordinary loads (lane (r = l % 16,
+// s = l / 16) reads the 16-byte chunks 4j + s of row r), as the verify's two
+// bodies do.
 template <bool NT>
 __device__ __forceinline__ float verify_twin_tile(__amdgpu_buffer_rsrc_t r, __amdgpu_buffer_rsrc_t wr, int lane,
                                                   int write_dw, float acc) {
   constexpr int pol = NT ? kNT : 0;
   int voff[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) voff[j] = NT ? lane * 16 + j * 1024 : (lane & 15) * kRowBytes + (4 * j + (lane >> 4)) * 16;
+  for (int j = 0; j < 8; ++j)
+    voff[j] = NT ? ((j & 3) * 4 + (lane >> 4)) * kRowBytes + ((j >> 2) * 16 + (lane & 15)) * 16
+                 : (lane & 15) * kRowBytes + (4 * j + (lane >> 4)) * 16;
   u32x4 a[8], b[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[j], 0, pol);

@@ -28,7 +28,7 @@
 // row, so the k-slot s of MFMA (j, e) holds element E*(4j+s)+e; B uses the
 // same permutation of K. Rows read with ordinary loads are loaded in that
 // layout; rows read non-temporally (the early rows of a large batch, see
-// verify_kernel) are loaded as whole rows and reach it through LDS.
+// verify_kernel) are loaded in row runs and reach it through LDS.
 //
 // Template parameters: S state element type, A activation type (q, k, v and
 // the key record / output when they share it), J 16-byte chunks per lane per
@@ -664,7 +664,7 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
       };
       auto store = [&](__amdgpu_buffer_rsrc_t r) {
         if constexpr (NT) {
-          // Whole rows, non-temporal: the folded chunks go back through LDS
+          // Row runs, non-temporal: the folded chunks go back through LDS
           // into the load layout (each lane writes the slots it read its
           // operands from). Stores of 64-byte pieces of 16 rows ran slower,
           // and non-temporal ones much slower: a synthetic twin of this

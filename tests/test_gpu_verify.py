@@ -78,7 +78,7 @@ def _run_and_check(P, dev, *, key_dtype=None, record_rows=None, packed=False, l2
     before = ckpt.clone()
     out, rec, planes = launch()
     assert torch.equal(ckpt, before), "verify must never write the checkpoint"
-    # The same launch with the state read non-temporally (whole-row loads
+    # The same launch with the state read non-temporally (row-run loads
     # turned into the operand layout through LDS) for every row, then for the
     # earlier half: the same bits as the ordinary loads.
     for retain in retain_settings(B, HV * V * K * ckpt.element_size())[:2]:
