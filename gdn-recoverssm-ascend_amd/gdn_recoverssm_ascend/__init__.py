@@ -38,13 +38,16 @@ def initialize():
 
 def set_state_cache_retain(nbytes: int) -> int:
     """Cache hint of this implementation (the reference has none): how many
-    bytes of checkpoint state each verify launch reads with ordinary loads,
-    counted from the end of its batch; earlier rows read their pages
-    non-temporally. Keep the default (256 MiB, the MI355X memory-side cache)
-    when a layer's commit directly follows its verify; set 0 when other
-    layers' verifies run in between (the model's decode step) or with the
-    deferred commit. Results are identical either way. Process-wide; returns
-    the previous value."""
+    bytes of checkpoint state each verify launch (``gdn_recoverssm_verify``,
+    ``gdn_recoverssm_verify_gated``) reads with ordinary loads, counted from
+    the end of its batch; earlier rows read their pages non-temporally. Keep
+    the default (256 MiB, the MI355X memory-side cache) when a layer's commit
+    directly follows its verify, so the commit finds the last-read pages
+    cached. When other layers' verifies run in between (the model's decode
+    step) nothing re-reads them soon; B=128 layers then ran fastest with
+    64 MiB. The deferred verify reads every row non-temporally whatever the
+    setting. Results are identical either way. Process-wide; returns the
+    previous value."""
     from . import _native
 
     if int(nbytes) < 0:
