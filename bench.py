@@ -13,6 +13,14 @@ block boundary, accepted lengths uniform in {0..4}, 6 padded rows.
 byte model below, computed from the seeded draws) divided by the measured step
 time, with every input resident in HBM before the timed region starts.
 Per-kernel durations come from HIP events on the stream the kernels run on.
+The verify runs with the library's default cache hint (the last 256 MiB of a
+batch's state read with ordinary loads, the rest non-temporally), so the
+commit finds the pages it re-reads in the memory-side cache;
+``disjoint_pools`` repeats the step on two batches with separate page pools
+taking turns, which leaves only that within-step reuse. The line also carries
+the other single-layer configurations, the deferred commit, the 48-layer
+decode loop (its verifies retain 64 MiB per layer) and the traffic twins of
+both kernels.
 
 Algorithmic bytes (f32 state, bf16 activations / keys):
   verify = B_valid*HV*V*K*4 (state, once)  + T*(2*H*K + HV*V)*2 (q, k, v)
