@@ -633,8 +633,12 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
   // DEFER: replay the pending accepted prefix on one block in registers,
   // h <- fma(c_t, k_t, h * d_t) as the fold does, storing the boundary snapshot
   // after `boundary_len` tokens and the final state after n (kernels.py:1242-1324).
-  // Both stores are issued on every path (an unused one reads as out of range)
-  // so the wait counts of the loads in flight never depend on the row.
+  // The final store is issued on every path (an unused one falls out of
+  // range) so the wait counts of the loads in flight do not depend on the row.
+  // The boundary snapshot's store, with its two LDS rounds, only runs on rows
+  // that have one (about one tile in seven at B=256): skipping the round trip
+  // elsewhere took the 48-layer deferred loop from 5.37-5.46 to 5.32 ms per
+  // step, which outweighs the stricter waits on the snapshot rows.
   auto fold_block = [&](int rb, uint4 (&buf)[J], const float (&pc)[QM]) {
     if constexpr (DEFER) {
       const int seg = pstore_b ? pblen : 0;
@@ -696,7 +700,7 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
         }
       };
       apply(0, seg);
-      store(rbnd);
+      if (pstore_b) store(rbnd);
       apply(seg, pn);
       store(rfin);
       // The window is verified from the folded tile as stored.
