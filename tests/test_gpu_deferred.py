@@ -301,8 +301,9 @@ def test_deferred_commit_equals_ordinary_flow(dev, seed, empty_row):
     got = _flow(w, dev, acc_steps, qsl_steps, deferred=True)
     _assert_flows_equal(ref, got)
     assert sum(int((h["plan"][2] > 0).sum()) for h in ref[0]) > 0
-    # Both state-load bodies of the verify: every row non-temporal, then the
-    # later half ordinary.
+    # The cache hint changes only the ordinary verify of each flow's first step
+    # (every row non-temporal, then the later half ordinary); the deferred
+    # verify reads every row non-temporally whatever it says.
     for retain in retain_settings(s.rows, s.value_heads * s.value_dim * s.key_dim * 4)[:2]:
         with state_cache_retain(retain):
             _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
@@ -333,7 +334,7 @@ def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act, s
     qsl_steps = [w.meta.query_start_loc.clone() for _ in range(steps)]
     ref = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
     _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
-    with state_cache_retain(0):  # every row's state read non-temporally
+    with state_cache_retain(0):  # the first step's ordinary verify: every row non-temporal
         _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
 
 
