@@ -6,6 +6,9 @@
 // (single context). Every index derived from data is bounds-checked against the
 // sizes the host passes; an out-of-range index makes the row a no-op (the
 // reference would read outside the tensor there).
+#include <algorithm>
+#include <vector>
+
 #include "plan_row.cuh"
 
 namespace gdn {
@@ -166,6 +169,78 @@ using namespace gdn;
 
 namespace gdn {
 
+// Byte range [lo, hi) of the elements a plan launch may touch in one array:
+// `n` elements of `esz` bytes at an element stride (empty for a null pointer
+// or no element); `n2` / `stride2` add a second dimension (the block table).
+struct PlanSpan {
+  uintptr_t lo = 0, hi = 0;
+  const char *what = "";
+};
+static PlanSpan plan_span(const char *what, const void *p, int64_t n, int64_t stride, int64_t esz, int64_t n2 = 1,
+                          int64_t stride2 = 0) {
+  PlanSpan s;
+  s.what = what;
+  if (!p || n <= 0 || n2 <= 0) return s;
+  int64_t lo = 0, hi = 0;  // element offsets of the extreme corners
+  for (int64_t a : {int64_t(0), (n - 1) * stride})
+    for (int64_t b : {int64_t(0), (n2 - 1) * stride2}) lo = std::min(lo, a + b), hi = std::max(hi, a + b);
+  const uintptr_t base = reinterpret_cast<uintptr_t>(p);
+  s.lo = base + uintptr_t(lo * esz);
+  s.hi = base + uintptr_t((hi + 1) * esz);
+  return s;
+}
+static bool spans_overlap(const PlanSpan &a, const PlanSpan &b) {
+  return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi;
+}
+
+// The plan's outputs must not share memory with its inputs or with each
+// other: a plan row reads the metadata of other rows (its request's accepted
+// count, the block table), and in the fused plan + fold launch the writer
+// workgroups store the plan while the folding workgroups plan their rows from
+// the same metadata, unordered against them.
+static bool plan_memory_disjoint(const gdn_plan_launch *L) {
+  const bool align = L->flags & GDN_PLAN_ALIGN;
+  auto esz = [](int32_t dt) { return int64_t(dt == GDN_DT_I64 ? 8 : 4); };
+  const int64_t rows = L->num_rows, entries = int64_t(L->num_groups) * L->plan_capacity;
+  std::vector<PlanSpan> in, outs;
+  in.push_back(plan_span("accepted counts", L->sampled, L->sampled_len, L->sampled_stride, esz(L->sampled_dtype)));
+  in.push_back(plan_span("request mapping", L->idx_mapping, L->idx_mapping_len, 1, esz(L->idx_mapping_dtype)));
+  for (int i = 0; i < L->num_groups; ++i) {
+    const gdn_plan_group &g = L->groups[i];
+    in.push_back(plan_span("state indices", g.state_indices, rows, g.si_stride, esz(g.si_dtype)));
+    in.push_back(plan_span("query offsets", g.query_start_loc, rows + 1, g.qsl_stride, esz(g.qsl_dtype)));
+    in.push_back(plan_span("request indices", g.request_indices, rows, g.map_stride, esz(g.map_dtype)));
+    if (align) {
+      in.push_back(plan_span("block table", g.block_table, g.table_rows, g.table_row_stride, esz(g.table_dtype),
+                             g.table_width, g.table_col_stride));
+      in.push_back(plan_span("computed tokens", g.num_computed, g.computed_len, g.computed_stride,
+                             esz(g.computed_dtype)));
+    }
+  }
+  const int32_t *plan_arrays[7] = {L->source_plan, L->lens_plan,  L->final_plan, L->boundary_plan,
+                                   L->boundary_lens_plan, L->valid_plan, L->col_plan};
+  for (const int32_t *p : plan_arrays) outs.push_back(plan_span("plan array", p, entries, 1, 4));
+  if ((L->flags & GDN_PLAN_PUBLISH) && align) {
+    outs.push_back(plan_span("persistent columns", L->persistent_cols, L->persistent_len, 1, 4));
+    outs.push_back(plan_span("persistent acceptance", L->persistent_accepted, L->persistent_len, 1, 4));
+  }
+  for (size_t i = 0; i < outs.size(); ++i) {
+    for (const PlanSpan &x : in) {
+      if (spans_overlap(outs[i], x)) {
+        set_error("plan: a %s output overlaps the %s it reads", outs[i].what, x.what);
+        return false;
+      }
+    }
+    for (size_t j = i + 1; j < outs.size(); ++j) {
+      if (spans_overlap(outs[i], outs[j])) {
+        set_error("plan: two plan outputs (%s, %s) overlap", outs[i].what, outs[j].what);
+        return false;
+      }
+    }
+  }
+  return true;
+}
+
 int make_plan_args(const gdn_plan_launch *L, PlanArgs *out) {
   if (!L) {
     set_error("plan: missing launch block");
@@ -219,6 +294,7 @@ int make_plan_args(const gdn_plan_launch *L, PlanArgs *out) {
     }
     a.groups[i] = g;
   }
+  if (!plan_memory_disjoint(L)) return GDN_ERR_INVALID;
   a.source = L->source_plan;
   a.lens = L->lens_plan;
   a.final_ = L->final_plan;

@@ -401,6 +401,18 @@ static int make_fold_args(const int64_t *state_addrs, const int64_t *state_block
               (long long)config[10], (long long)K);
     return GDN_ERR_UNSUPPORTED;
   }
+  // Record loads take 32-bit offsets from each (row, head)'s first token:
+  // the token strides must be non-negative and a window's records must lie
+  // far below the out-of-range offset.
+  const int64_t key_bytes = ext->key_dtype == GDN_DT_F32 ? 4 : 2;
+  const int64_t kp_max = 256;
+  if (config[12] < 0 || config[14] < 0 || (query_len * config[12] + V) * 4 >= kFoldOutOfRange ||
+      (query_len * config[14] + kp_max) * key_bytes >= kFoldOutOfRange) {
+    set_error("fold: record token strides (correction %lld, key %lld) must be non-negative and span under 2 GiB "
+              "per window",
+              (long long)config[12], (long long)config[14]);
+    return GDN_ERR_UNSUPPORTED;
+  }
   FoldArgs a{};
   a.state_addrs = state_addrs;
   a.state_bs = state_block_strides;
@@ -450,14 +462,10 @@ static int launch_fold(const gdn_fold_ext *ext, int64_t grid, size_t lds, const 
   }
   auto s = static_cast<hipStream_t>(stream);
   const dim3 g{unsigned(grid)};
-  // Records first for grids of a few rounds, when they fit the early passes
-  // and their token windows the 32-bit offsets of a buffer resource.
-  const int64_t key_bytes = ext->key_dtype == GDN_DT_F32 ? 4 : 2;
+  // Records first for grids of a few rounds, when they fit the early passes.
+  // (make_fold_args has checked that every window's records fit 32-bit offsets.)
   const bool early = grid <= kEarlyMaxGrid && a.Q * a.V <= kRecPasses * kFoldThreads &&
-                     a.Q * a.KP <= kRecPasses * kFoldThreads &&
-                     (a.Q * a.corr_token_stride + a.V) * 4 < kFoldOutOfRange &&
-                     (a.Q * a.key_token_stride + a.KP) * key_bytes < kFoldOutOfRange && a.corr_token_stride >= 0 &&
-                     a.key_token_stride >= 0;
+                     a.Q * a.KP <= kRecPasses * kFoldThreads;
   switch (ext->state_dtype) {
     case GDN_DT_BF16: launch_fold_state<bf16>(early, ext->key_dtype, g, lds, s, a, plan, writers); break;
     case GDN_DT_F16: launch_fold_state<f16>(early, ext->key_dtype, g, lds, s, a, plan, writers); break;

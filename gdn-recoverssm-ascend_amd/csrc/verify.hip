@@ -218,7 +218,9 @@ static int verify_impl(const void *q, const void *k, const void *v, const void *
     a.nt_rows = int32_t(rows);
   } else {
     const int64_t row_state = value_heads * V * state_vs * (E == 4 ? 4 : 2);
-    const int64_t keep = state_cache_retain();
+    const int64_t keep = ext->state_cache_retain > 0   ? ext->state_cache_retain
+                         : ext->state_cache_retain < 0 ? 0
+                                                       : state_cache_retain();
     const int64_t keep_rows = row_state <= 0 ? rows : keep / row_state + (keep % row_state != 0);
     a.nt_rows = int32_t(rows > keep_rows ? rows - keep_rows : 0);
   }

@@ -60,6 +60,7 @@ class VerifyExt(ctypes.Structure):
         ("qk_l2norm", c_i32),
         ("key_per_value_head", c_i32),
         ("out_dtype", c_i32),
+        ("state_cache_retain", c_i64),
     ]
 
 

@@ -74,6 +74,11 @@ typedef struct gdn_verify_ext {
   int32_t qk_l2norm;        /* 1: normalise q and k in-kernel (eps 1e-6), kernels.py:645-648 */
   int32_t key_per_value_head; /* 1: packed record layout, one key per value head, kernels.py:687-697 */
   int32_t out_dtype;        /* out: F32 / BF16 / F16 (kernels.py:657 stores in out's own dtype) */
+  int64_t state_cache_retain; /* no counterpart in the reference: this call's cache hint, the bytes
+                                 of state read with ordinary loads from the end of the batch (see
+                                 gdn_recoverssm_set_state_cache_retain); 0: the process-wide
+                                 setting; negative: none (every row non-temporal). Results do not
+                                 depend on it. gdn_recoverssm_verify_deferred ignores it. */
 } gdn_verify_ext;
 
 typedef struct gdn_fold_ext {
@@ -177,19 +182,23 @@ int gdn_recoverssm_verify_deferred(const void *q, const void *k, const void *v, 
                                    int64_t config_len, float scale, const gdn_verify_ext *ext,
                                    const gdn_pending_commit *pending, void *stream);
 
-/* Default of gdn_recoverssm_set_state_cache_retain: 256 MiB, the MI355X's
- * memory-side (Infinity) cache. */
-#define GDN_STATE_CACHE_RETAIN_DEFAULT (256LL << 20)
+/* Default of gdn_recoverssm_set_state_cache_retain: 64 MiB, measured best for
+ * the verifies of a model's decode step, where no commit re-reads a layer's
+ * pages right after its verify (the commit comes after every layer). */
+#define GDN_STATE_CACHE_RETAIN_DEFAULT (64LL << 20)
 
 /* No counterpart in the reference (a cache hint of this implementation).
  * How many bytes of checkpoint state a verify launch (gdn_recoverssm_verify,
  * gdn_recoverssm_verify_gated) reads with ordinary loads, counted from the end
- * of its batch: the rows before them read their pages non-temporally. A
- * commit that reads the same pages right after the verify (verify, sampling,
- * commit of one layer) finds the last-read part in the memory-side cache.
- * gdn_recoverssm_verify_deferred reads and writes every row non-temporally
- * whatever the setting (nothing re-reads its pages soon). Results do not
- * depend on it. Process-wide; returns the previous value, or -1 (nothing
+ * of its batch: the rows before them read their pages non-temporally. What
+ * the ordinary loads leave in the memory-side (Infinity) cache, 256 MB on
+ * MI355X, is what a commit reading the same pages right after the verify
+ * finds there (a single layer's verify, sampling, commit: retaining 256 MiB
+ * suits it); in a decode step nothing re-reads them soon, and a quarter of a
+ * B=128 layer's pages read ordinarily measured fastest. gdn_recoverssm_verify_deferred
+ * reads and writes every row non-temporally whatever the setting. Results do
+ * not depend on it. Process-wide, used by calls whose gdn_verify_ext leaves
+ * state_cache_retain at 0; returns the previous value, or -1 (nothing
  * changed) for a negative `bytes`. */
 int64_t gdn_recoverssm_set_state_cache_retain(int64_t bytes);
 

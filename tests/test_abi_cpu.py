@@ -44,14 +44,14 @@ def test_abi_version_and_error_channel():
 
 
 def test_state_cache_retain_setting():
-    """The verify cache hint: default 256 MiB, returns the previous value,
+    """The verify cache hint: default 64 MiB, returns the previous value,
     rejects a negative byte count without changing the setting."""
     import gdn_recoverssm_ascend as G
 
     lib = N.load()
     prev = lib.gdn_recoverssm_set_state_cache_retain(0)
     try:
-        assert prev == 256 << 20
+        assert prev == 64 << 20
         assert lib.gdn_recoverssm_set_state_cache_retain(-5) == -1
         assert G.set_state_cache_retain(12345) == 0
         with pytest.raises(ValueError, match="GDN RecoverSSM"):
@@ -59,6 +59,29 @@ def test_state_cache_retain_setting():
         assert G.set_state_cache_retain(prev) == 12345
     finally:
         lib.gdn_recoverssm_set_state_cache_retain(prev)
+
+
+def test_per_call_cache_hint_field():
+    """A call's own cache hint rides in gdn_verify_ext: 0 selects the
+    process-wide setting, a positive byte count is used as given, and a
+    request to retain nothing becomes a negative field; a negative request
+    is refused before anything is built."""
+    import torch
+
+    from gdn_recoverssm_ascend.kernels import _retain_arg, _VerifyCall
+
+    assert N.VerifyExt.state_cache_retain.offset == 56 and ctypes.sizeof(N.VerifyExt) == 64
+
+    def field(nbytes):
+        c = _VerifyCall(*([None] * 9), 4, True, None, None, _retain_arg(nbytes))
+        return c.retain_field
+
+    assert field(None) == 0
+    assert field(256 << 20) == 256 << 20
+    assert field(0) == -1
+    with pytest.raises(ValueError, match="GDN RecoverSSM: the retained state bytes"):
+        _retain_arg(-1)
+    del torch
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
@@ -94,17 +117,67 @@ def test_invalid_arguments_are_rejected_before_any_launch():
                                       ctypes.byref(fext), None)
     assert st == N.GDN_ERR_INVALID and b"num_groups" in lib.gdn_recoverssm_last_error()
     g0 = groups[0]
-    g0.state_indices = g0.query_start_loc = 8  # never dereferenced: the call is rejected before a launch
+    # Addresses that are never dereferenced: every call here is rejected before a launch.
+    g0.state_indices, g0.query_start_loc = 0x60000, 0x70000
     g0.si_dtype = g0.qsl_dtype = 3
-    launch = N.PlanLaunch(sampled=8, sampled_len=4, sampled_dtype=3, num_groups=1,
-                          groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), lens_plan=8, final_plan=8,
-                          boundary_plan=8, boundary_lens_plan=8, num_rows=4, plan_capacity=4, spec_query_len=4)
+    g0.si_stride = g0.qsl_stride = 1
+    launch = N.PlanLaunch(sampled=0x50000, sampled_len=4, sampled_stride=1, sampled_dtype=3, num_groups=1,
+                          groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), lens_plan=0x10000,
+                          final_plan=0x20000, boundary_plan=0x30000, boundary_lens_plan=0x40000, num_rows=4,
+                          plan_capacity=4, spec_query_len=4)
     tables = [8] * 8
     fcfg = N.i64_array([4, 1, 4, 2, 4, 16, 4, 8, 0, 128 * 128, 128, 512, 128, 256, 128, 4, 1])
     fext1 = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1)
     st = lib.gdn_recoverssm_plan_fold(ctypes.byref(launch), None, None, None, None, *tables, None, fcfg, 17,
                                       ctypes.byref(fext1), None)
     assert st == N.GDN_ERR_INVALID and b"differ from the plan" in lib.gdn_recoverssm_last_error()
+    # Record token strides outside a buffer resource's 32-bit window are refused.
+    for field, value in ((12, -1), (14, -128), (12, 1 << 29), (14, 1 << 30)):
+        bad = list(fcfg)
+        bad[field] = value
+        st = lib.gdn_recoverssm_plan_fold(ctypes.byref(launch), None, None, None, None, *tables, None,
+                                          N.i64_array(bad), 17, ctypes.byref(fext1), None)
+        assert st == N.GDN_ERR_UNSUPPORTED and b"record token strides" in lib.gdn_recoverssm_last_error(), field
+
+
+def test_plan_outputs_must_not_overlap_its_inputs():
+    """A plan whose output arrays share memory with the metadata it reads
+    (or with each other) is refused before any launch: in the fused plan +
+    fold launch the writer workgroups would store into what the folding
+    workgroups are still planning from."""
+    lib = N.load()
+    groups = N.PlanGroups()
+    g0 = groups[0]
+    g0.state_indices, g0.query_start_loc = 0x60000, 0x70000
+    g0.si_dtype = g0.qsl_dtype = 3
+    g0.si_stride = g0.qsl_stride = 1
+    base = dict(sampled=0x50000, sampled_len=4, sampled_stride=1, sampled_dtype=3, num_groups=1,
+                groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), lens_plan=0x10000, final_plan=0x20000,
+                boundary_plan=0x30000, boundary_lens_plan=0x40000, num_rows=4, plan_capacity=4, spec_query_len=4)
+    fcfg = N.i64_array([4, 1, 4, 2, 4, 16, 4, 8, 0, 128 * 128, 128, 512, 128, 256, 128, 4, 1])
+    fext = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1)
+
+    def call(**over):
+        launch = N.PlanLaunch(**dict(base, **over))
+        return lib.gdn_recoverssm_plan_fold(ctypes.byref(launch), None, None, None, None, *([8] * 8), None, fcfg, 17,
+                                            ctypes.byref(fext), None)
+
+    # the final pages written over the state indices the rows are planned from
+    assert call(final_plan=0x60000) == N.GDN_ERR_INVALID
+    assert b"overlaps the state indices" in lib.gdn_recoverssm_last_error()
+    # lengths written over the accepted counts, one element in
+    assert call(lens_plan=0x50000 + 12) == N.GDN_ERR_INVALID
+    assert b"overlaps the accepted counts" in lib.gdn_recoverssm_last_error()
+    # two outputs sharing memory
+    assert call(boundary_plan=0x20000 + 8) == N.GDN_ERR_INVALID
+    assert b"two plan outputs" in lib.gdn_recoverssm_last_error()
+    # adjacent but disjoint ranges pass this check (and fail the next one)
+    assert call(lens_plan=0x50000 + 16) == N.GDN_ERR_INVALID
+    assert b"differ from the plan" in lib.gdn_recoverssm_last_error()
+    # the same through the separate plan entry
+    st = lib.gdn_recoverssm_plan(0x50000, 3, 1, 4, groups, 1, None, 0x70000 + 4, 0x20000, 0x30000, 0x40000, None,
+                                 None, None, 3, 0, None, None, 0, 4, 4, 0, 4, 0, None)
+    assert st == N.GDN_ERR_INVALID and b"overlaps the query offsets" in lib.gdn_recoverssm_last_error()
 
 
 def test_commit_noalloc_rejects_before_touching_the_device():
@@ -161,6 +234,7 @@ _LAYOUT_PROBE = r"""
 #define F(T, f) printf("%s.%s %zu\n", #T, #f, offsetof(T, f));
 int main(void) {
   printf("gdn_verify_ext %zu\n", sizeof(gdn_verify_ext));
+  F(gdn_verify_ext, state_cache_retain)
   printf("gdn_fold_ext %zu\n", sizeof(gdn_fold_ext));
   printf("gdn_plan_group %zu\n", sizeof(gdn_plan_group));
   printf("gdn_gating_ext %zu\n", sizeof(gdn_gating_ext));
