@@ -9,6 +9,7 @@ the HIP library is loaded on first launch and its absence is an error.
 
 from .grouped_commit import (  # noqa: F401
     CommitEntry,
+    DeferredGroupedCommit,
     GroupedCommitBucket,
     GroupedCommitCoordinator,
     prepare_grouped_commit,
@@ -40,14 +41,16 @@ def set_state_cache_retain(nbytes: int) -> int:
     """Cache hint of this implementation (the reference has none): how many
     bytes of checkpoint state each verify launch (``gdn_recoverssm_verify``,
     ``gdn_recoverssm_verify_gated``) reads with ordinary loads, counted from
-    the end of its batch; earlier rows read their pages non-temporally. Keep
-    the default (256 MiB, the MI355X memory-side cache) when a layer's commit
-    directly follows its verify, so the commit finds the last-read pages
-    cached. When other layers' verifies run in between (the model's decode
-    step) nothing re-reads them soon; B=128 layers then ran fastest with
-    64 MiB. The deferred verify reads every row non-temporally whatever the
-    setting. Results are identical either way. Process-wide; returns the
-    previous value."""
+    the end of its batch; earlier rows read their pages non-temporally. This
+    is the process-wide setting, used by every call that does not pass its
+    own ``state_cache_retain``. The default, 64 MiB, suits the model's decode
+    step, where other layers' verifies run before any commit re-reads a
+    layer's pages (B=128 layers ran fastest with it). A caller whose commit
+    directly follows the verify of the same pages (one layer's verify,
+    sampling, commit) gains from 256 MiB, the MI355X memory-side cache: the
+    commit then finds the last-read pages there. The deferred verify reads
+    every row non-temporally whatever the setting. Results are identical
+    either way. Returns the previous value."""
     from . import _native
 
     if int(nbytes) < 0:
@@ -57,6 +60,7 @@ def set_state_cache_retain(nbytes: int) -> int:
 
 __all__ = [
     "CommitEntry",
+    "DeferredGroupedCommit",
     "GDNRecoverSSMCommitContext",
     "GroupedCommitBucket",
     "GroupedCommitCoordinator",

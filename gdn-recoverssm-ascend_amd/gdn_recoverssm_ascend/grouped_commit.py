@@ -23,9 +23,10 @@ from typing import Any
 import torch
 
 from . import _native as N
-from ._rules import enforce, fail
+from ._rules import enforce, fail, require
 from ._tables import LayerPages
-from .kernels import NULL_BLOCK_ID, _conv_spec, _fill_plan_group, _fuse_plan_fold, _LaunchSpec, _make_fold_spec
+from .kernels import (_FOLD_LENGTHS_ARG, NULL_BLOCK_ID, PendingCommit, _conv_spec, _fill_plan_group,
+                      _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _unapplied_lengths)
 
 logger = logging.getLogger("gdn_recoverssm_ascend.grouped_commit")
 
@@ -273,6 +274,118 @@ class GroupedCommitBucket:
 
 
 # ---------------------------------------------------------------------------
+# Deferred grouped commit (docs/GDN-RecoverSSM-实现方案.md:515-527, 563-568)
+# ---------------------------------------------------------------------------
+
+
+class DeferredGroupedCommit:
+    """One step's grouped commit with its folds left to the next step's
+    verifies (``gdn_recoverssm_verify_deferred``): every bucket's plan is
+    stored, the conv states are compacted and the align columns published,
+    exactly as ``GroupedCommitCoordinator.commit`` does them; only the folds
+    wait.
+
+    ``pending(i)`` gives one ``PendingCommit`` per layer of the step's i-th
+    committing cache group (metadata order). All share one row map (next row
+    -> pending row), the in-place map until ``continue_with`` re-keys it by
+    request. Every pending row must be folded once before its pages are
+    reused: by the next verify that continues it, or here, by ``settle``
+    (every row the next verifies will not apply, decided on the device) or
+    ``flush`` (given rows, or all). The object stays valid until the same
+    contexts commit again (their plan arrays are reused then): a deferred
+    flow alternates two sets of contexts, as the pending step's records must
+    not be the ones the next verify writes.
+    """
+
+    def __init__(self, entries, placed, rows, device):
+        self._entries = tuple(entries)
+        self._placed = tuple(placed)  # per entry: (bucket, its group in the bucket, fold spec)
+        self.num_rows = int(rows)
+        self.rows = torch.arange(max(1, self.num_rows), dtype=torch.int32, device=device)
+
+    def __len__(self):
+        return len(self._entries)
+
+    def _plan(self, i):
+        bucket, g, _ = self._placed[i]
+        seg = slice(g * bucket.capacity, (g + 1) * bucket.capacity)
+        return tuple(t[seg] for t in (bucket.source, bucket.length, bucket.final, bucket.boundary,
+                                      bucket.boundary_len))
+
+    def pending(self, i) -> tuple:
+        """The pending commits of group ``i``'s layers, in its context's layer order."""
+        plan = self._plan(i)
+        return tuple(PendingCommit(self.rows, *plan, rec, num_rows=self.num_rows)
+                     for rec in self._entries[i].context.records)
+
+    def continue_with(self, previous_requests, next_requests) -> list:
+        """Key the pending rows by request for the next batch (host-side ids,
+        as ``continue_pending``): ``previous_requests[r]`` is the request of
+        pending row r, ``next_requests[b]`` that of next row b. Returns the
+        sorted pending rows whose request left; ``settle`` or ``flush`` must
+        fold them."""
+        require(len(previous_requests) >= self.num_rows, "previous request ids do not cover the pending rows")
+        where = {}
+        for r, req in enumerate(previous_requests[:self.num_rows]):
+            require(req not in where, f"request {req!r} appears twice in the pending step")
+            where[req] = r
+        seen, mapping = set(), []
+        for req in next_requests:
+            require(req not in seen, f"request {req!r} appears twice in the next batch")
+            seen.add(req)
+            mapping.append(where.get(req, -1))
+        self.rows = torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=self.rows.device)
+        return sorted(r for req, r in where.items() if req not in seen)
+
+    def _fold(self, bucket, fold, lengths) -> None:
+        args = list(fold.args)
+        args[_FOLD_LENGTHS_ARG] = lengths.data_ptr()
+        _LaunchSpec(fold.name, fold.fn, tuple(args), fold.device, keepalive=fold.keepalive + (lengths,)).launch()
+
+    def _buckets(self):
+        seen = {}
+        for i, (bucket, g, fold) in enumerate(self._placed):
+            seen.setdefault(id(bucket), (bucket, fold, []))[2].append((i, g))
+        return seen.values()
+
+    def flush(self, rows=None) -> None:
+        """Fold the given pending rows (every planned row when None) of every
+        group now, with the ordinary fold."""
+        pick = None
+        if rows is not None:
+            pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
+            require(bool(((pick >= 0) & (pick < self.num_rows)).all()), "flushed rows must be rows of the pending plan")
+            if pick.numel() == 0:
+                return
+        for bucket, fold, members in self._buckets():
+            if pick is None:
+                lengths = bucket.length
+            else:
+                lengths = torch.zeros_like(bucket.length)
+                for _, g in members:
+                    idx = (pick + g * bucket.capacity).to(lengths.device)
+                    lengths[idx] = bucket.length[idx]
+            self._fold(bucket, fold, lengths)
+
+    def settle(self, next_metadata) -> None:
+        """Fold now every pending row that the next step's deferred verifies
+        will not apply: group i of ``next_metadata`` (the next step's
+        metadata, same group order) continues pending row ``rows[b]`` in its
+        row b only when its state index there is that commit's final page.
+        Decided on the device; call it before the next verifies."""
+        nxt = _step_entries(next_metadata)
+        require(len(nxt) == len(self._entries), "the next step has another number of committing groups")
+        for bucket, fold, members in self._buckets():
+            lengths = bucket.length.clone()
+            for i, g in members:
+                seg = slice(g * bucket.capacity, (g + 1) * bucket.capacity)
+                si = nxt[i].payload.state_indices
+                require(self.rows.shape[0] >= si.shape[0], "the pending row map does not cover the next batch")
+                lengths[seg] = _unapplied_lengths(bucket.length[seg], bucket.final[seg], self.num_rows, self.rows, si)
+            self._fold(bucket, fold, lengths)
+
+
+# ---------------------------------------------------------------------------
 # The coordinator
 # ---------------------------------------------------------------------------
 
@@ -314,6 +427,7 @@ class GroupedCommitCoordinator:
 
     def __init__(self):
         self._buckets: dict = {}        # context identities -> bucket, the last step's only
+        self._previous: dict = {}       # a deferred flow's step before it (its contexts alternate)
         self._logged_shapes: set = set()
         self.steps = 0
         self._note_step(0, 0, 0)
@@ -327,6 +441,8 @@ class GroupedCommitCoordinator:
         key = tuple(map(id, contexts))
         if key in self._buckets:
             return self._buckets[key]
+        if key in self._previous:
+            return self._previous[key]
         # A bucket built by prepare_grouped_commit for exactly these contexts is adopted.
         prepared = getattr(members[0].metadata.recoverssm_builder, "_prepared_group_bucket", None)
         if prepared is not None and tuple(map(id, prepared.contexts)) == key:
@@ -334,19 +450,46 @@ class GroupedCommitCoordinator:
         return GroupedCommitBucket(contexts)
 
     def commit(self, metadata, sampled, idx_mapping, persistent_cols, persistent_accepted):
+        self._commit(metadata, sampled, idx_mapping, persistent_cols, persistent_accepted, deferred=False)
+
+    def commit_deferred(self, metadata, sampled, idx_mapping, persistent_cols,
+                        persistent_accepted) -> DeferredGroupedCommit | None:
+        """``commit`` with the folds left to the next step's verifies: plans,
+        conv compaction and publication now, and a ``DeferredGroupedCommit``
+        that hands each layer its ``PendingCommit`` (None when no group
+        commits). The groups must share one set of logical rows and typed
+        record buffers. Buckets of the previous step are kept as well, so a
+        flow that alternates two sets of contexts reuses both."""
+        return self._commit(metadata, sampled, idx_mapping, persistent_cols, persistent_accepted, deferred=True)
+
+    def _commit(self, metadata, sampled, idx_mapping, persistent_cols, persistent_accepted, *, deferred):
         entries = _step_entries(metadata)
         if not entries:
             self._note_step(0, 0, 0)
-            return
+            return None
         align = _check_step(entries)
+        if deferred:
+            first = _rows_of(entries[0])
+            enforce((
+                ("the deferred grouped commit needs every group on one set of logical rows",
+                 lambda: isinstance(first, _LogicalRows) and all(_rows_of(e) == first for e in entries)),
+                ("the deferred commit needs typed record buffers",
+                 lambda: all(e.context.record_layout == "soa" for e in entries)),
+            ))
         buckets = _partition(entries)
         used = {}
+        placed = {}
         launches = 0
         for members in buckets:
             bucket = self._bucket_for(members)
             used[tuple(id(e.context) for e in members)] = bucket
             specs = bucket.make_specs(members, sampled, idx_mapping, persistent_cols, persistent_accepted,
-                                      publish_align=len(buckets) == 1)
+                                      publish_align=len(buckets) == 1, fuse_plan_fold=not deferred)
+            if deferred:
+                plan, compact, fold = specs
+                specs = (plan, compact)
+                for g, e in enumerate(members):
+                    placed[id(e)] = (bucket, g, fold)
             for spec in specs:
                 spec.launch()
             launches += len(specs)
@@ -356,13 +499,19 @@ class GroupedCommitCoordinator:
             _publish_spec(tuple(used.values()), entries[0].payload.request_indices, idx_mapping, persistent_cols,
                           persistent_accepted, rows).launch()
             launches += 1
+        self._previous = self._buckets if deferred else {}
         self._buckets = used
         self.steps += 1
         self._note_step(launches, len(entries), rows)
-        shape = (len(entries), len(buckets), launches)
+        shape = (len(entries), len(buckets), launches, deferred)
         if shape not in self._logged_shapes:  # once per step shape
             self._logged_shapes.add(shape)
-            logger.info("grouped RecoverSSM commit: %d cache groups in %d buckets, %d launches", *shape)
+            logger.info("grouped RecoverSSM commit%s: %d cache groups in %d buckets, %d launches",
+                        " (folds deferred)" if deferred else "", *shape[:3])
+        if not deferred:
+            return None
+        device = entries[0].context.checkpoints[0].device
+        return DeferredGroupedCommit(entries, [placed[id(e)] for e in entries], rows, device)
 
 
 # ---------------------------------------------------------------------------
@@ -450,6 +599,7 @@ def prepare_grouped_commit(builders, block_tables=None, *, num_computed_tokens=N
 
 __all__ = [
     "CommitEntry",
+    "DeferredGroupedCommit",
     "GroupedCommitBucket",
     "GroupedCommitCoordinator",
     "prepare_grouped_commit",

@@ -34,7 +34,7 @@ from typing import Any
 import torch
 
 from . import _native as N
-from ._rules import enforce, require
+from ._rules import enforce, fail, require
 from ._tables import LayerPages, check_layers, record_planes
 
 # vLLM's physical null page (vllm.v1.attention.backends.utils.NULL_BLOCK_ID).
@@ -182,11 +182,21 @@ class _VerifyCall:
     Sizes are read lazily, so each rule only touches what the rules before it
     have established."""
 
-    def __init__(self, g, beta, q, k, v, checkpoint, records, qsl, indices, window, normalized, out, gating):
+    def __init__(self, g, beta, q, k, v, checkpoint, records, qsl, indices, window, normalized, out, gating,
+                 retain=None):
         self.g, self.beta, self.q, self.k, self.v = g, beta, q, k, v
         self.checkpoint, self.records, self.qsl, self.indices = checkpoint, records, qsl, indices
         self.window, self.normalized, self.out, self.gating = int(window), normalized, out, gating
         self.typed = isinstance(records, ReplayRecordBuffers)
+        self.retain = retain
+
+    @property
+    def retain_field(self) -> int:
+        """The ABI's per-call cache hint: 0 for the process-wide setting, the
+        byte count when positive, -1 for none."""
+        if self.retain is None:
+            return 0
+        return int(self.retain) if int(self.retain) > 0 else -1
 
     tokens = cached_property(lambda c: c.q.shape[1])
     H = cached_property(lambda c: c.q.shape[2])
@@ -297,7 +307,7 @@ def _verify_spec(c: _VerifyCall, out, scale, *, pending=None) -> _LaunchSpec:
         key_record_dtype=N.dtype_code(torch.float32 if p.packed else p.key.dtype),
         qsl_dtype=N.dtype_code(c.qsl.dtype), index_dtype=N.dtype_code(c.indices.dtype),
         qk_l2norm=0 if c.normalized else 1, key_per_value_head=1 if p.packed else 0,
-        out_dtype=N.dtype_code(out.dtype),
+        out_dtype=N.dtype_code(out.dtype), state_cache_retain=c.retain_field,
     )
     cfg = N.i64_array(config)
     lib = _lib()
@@ -366,6 +376,7 @@ def gdn_recoverssm_verify(
     scale: float | None = None,
     qk_already_normalized: bool = True,
     out: torch.Tensor | None = None,
+    state_cache_retain: int | None = None,
     _collect: list | None = None,
 ) -> torch.Tensor:
     """Verify a speculative window from each row's checkpoint page, which is
@@ -379,10 +390,19 @@ def gdn_recoverssm_verify(
     outputs, no records). ``scale`` defaults to K^-0.5. With
     ``qk_already_normalized=False`` q and k are L2-normalised in the kernel
     (eps 1e-6). Returns ``out`` [1, T, HV, V], allocated when not given.
+    ``state_cache_retain`` (no counterpart in the reference) is this call's
+    cache hint in bytes (see ``set_state_cache_retain``; None: the
+    process-wide setting); results do not depend on it.
     """
     c = _VerifyCall(g, beta, q, k, v, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
-                    qk_already_normalized, out, None)
+                    qk_already_normalized, out, None, _retain_arg(state_cache_retain))
     return _run_verify(c, scale, out, _collect)
+
+
+def _retain_arg(nbytes):
+    if nbytes is not None and int(nbytes) < 0:
+        fail("the retained state bytes must be >= 0")
+    return None if nbytes is None else int(nbytes)
 
 
 def gdn_recoverssm_verify_gated(
@@ -404,6 +424,7 @@ def gdn_recoverssm_verify_gated(
     softplus_beta: float = 1.0,
     softplus_threshold: float = 20.0,
     out: torch.Tensor | None = None,
+    state_cache_retain: int | None = None,
     _collect: list | None = None,
 ) -> torch.Tensor:
     """Verify with the layer's gating producer (and by default the q/k L2
@@ -424,7 +445,7 @@ def gdn_recoverssm_verify_gated(
     ))
     gating = (A_log, dt_bias, float(softplus_beta), float(softplus_threshold))
     c = _VerifyCall(a, b, q, k, v, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
-                    qk_already_normalized, out, gating)
+                    qk_already_normalized, out, gating, _retain_arg(state_cache_retain))
     return _run_verify(c, scale, out, _collect)
 
 
@@ -475,6 +496,9 @@ def continue_pending(pending: Sequence[PendingCommit], previous_requests: Sequen
     request, -1 for a new request) and the sorted pending rows whose request
     is not in the next batch: their commits are applied by no verify, so
     ``flush_deferred(rows=...)`` must fold them before their pages are reused.
+    ``settle_deferred(next_state_indices, rows)`` folds those rows and also
+    the continued ones whose next state index is not the pending final page
+    (which the verify does not apply either), deciding on the device.
     """
     require(len(pending) > 0, "no pending commits to continue")
     num_rows = int(pending[0].num_rows)
@@ -565,6 +589,27 @@ def gdn_recoverssm_verify_deferred(
     c = _VerifyCall(g, beta, q, k, v, checkpoint_state, replay_cache, query_start_loc, state_indices, spec_query_len,
                     qk_already_normalized, out, None)
     return _run_verify(c, scale, out, _collect, pending=(struct, (pending, rec)))
+
+
+def _unapplied_lengths(lengths: torch.Tensor, finals: torch.Tensor, num_rows: int, rows: torch.Tensor,
+                       next_state_indices: torch.Tensor) -> torch.Tensor:
+    """The plan's lengths with every pending row that a next row applies set
+    to 0 (device ops only). Next row b applies pending row r = rows[b] when
+    0 <= r < num_rows and next_state_indices[b] == finals[r], the deferred
+    verify's own test; its other tests (accepted length 1..Q, pages in range)
+    are the fold's as well, so a row failing them is a no-op either way."""
+    nb = next_state_indices.shape[0]
+    out = lengths.clone()
+    if nb == 0 or num_rows == 0:
+        return out
+    r = rows[:nb].to(torch.int64)
+    ok = (r >= 0) & (r < num_rows)
+    safe = torch.where(ok, r, torch.zeros_like(r))
+    ok = ok & (next_state_indices.to(torch.int64) == finals[safe].to(torch.int64))
+    applied = torch.zeros(num_rows + 1, dtype=torch.int32, device=lengths.device)
+    applied.scatter_(0, torch.where(ok, r, torch.full_like(r, num_rows)), 1)
+    out[:num_rows] = torch.where(applied[:num_rows] > 0, torch.zeros_like(out[:num_rows]), out[:num_rows])
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -999,6 +1044,30 @@ class GDNRecoverSSMCommitContext:
                 self.boundary_recovery_lens)
         return tuple(PendingCommit(self.pending_rows, *plan, rec, num_rows=self._deferred_rows)
                      for rec in self.records)
+
+    def settle_deferred(self, next_state_indices: torch.Tensor, rows: torch.Tensor | None = None,
+                        _collect: list | None = None) -> None:
+        """Fold now, with the ordinary fold, every row of the last
+        ``commit_deferred`` plan that the next deferred verify will not apply:
+        the next verify applies pending row ``r`` only through a next row
+        ``b`` with ``rows[b] == r`` whose state index ``next_state_indices[b]``
+        is that commit's final page. Rows whose request left, and continued
+        requests whose next state index names another page, are folded here,
+        so no commit is lost. Decided on the device (no host synchronisation);
+        call it before the next verify. ``rows`` is the row map of the
+        pending commits (``continue_pending``), the in-place map by default.
+        """
+        spec = getattr(self, "_deferred_fold", None)
+        require(spec is not None, "no deferred commit to flush")
+        num = self._deferred_rows
+        rows = self.pending_rows if rows is None else rows
+        require(next_state_indices.ndim == 1 and rows.shape[0] >= next_state_indices.shape[0],
+                "the pending row map does not cover the next batch")
+        lengths = _unapplied_lengths(self.commit_lens, self.final_state_indices, num, rows, next_state_indices)
+        args = list(spec.args)
+        args[_FOLD_LENGTHS_ARG] = lengths.data_ptr()
+        spec = _LaunchSpec(spec.name, spec.fn, tuple(args), spec.device, keepalive=spec.keepalive + (lengths,))
+        _submit(spec, _collect)
 
     def flush_deferred(self, rows: Sequence[int] | torch.Tensor | None = None, _collect: list | None = None) -> None:
         """Apply the last ``commit_deferred`` plan with the ordinary fold.
