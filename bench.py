@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--deferred", action="store_true",
                     help="decode-loop workloads: fold each commit into the next step's verify")
+    ap.add_argument("--groups", type=int, default=None,
+                    help="decode-loop workloads: commit through the grouped coordinator, the layers in this many "
+                         "cache groups")
     ap.add_argument("--loop-steps", type=int, default=None,
                     help="decode-loop workloads: speculative steps to time (default: the workload's own)")
     ap.add_argument("--kernel-only", action="store_true", help="time the step and its kernels only (no conv, gated, deferred or other-configuration lines)")
@@ -203,10 +206,7 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     # The verify reads the rows before the last `retain` bytes of state
     # non-temporally (row runs) and the rest in the operand layout; the twin
     # does the same for the same tiles.
-    from gdn_recoverssm_ascend import set_state_cache_retain
-
-    retain = set_state_cache_retain(0)
-    set_state_cache_retain(retain)
+    retain = STEP_STATE_RETAIN
     keep_rows = -(-retain // (HV * V * K * 4))
     nt_rows = max(0, B - keep_rows)
     nt_tiles = int(valid[:nt_rows].sum()) * HV
@@ -330,7 +330,7 @@ def other_configs(args, timer, skip):
         specs: list = []
         gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0],
                               replay_cache=rec, query_start_loc=m.query_start_loc, state_indices=m.state_indices,
-                              spec_query_len=Q, out=out, _collect=specs)
+                              spec_query_len=Q, out=out, state_cache_retain=STEP_STATE_RETAIN, _collect=specs)
         specs += list(ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
                                             block_table=m.block_table if align else None,
                                             num_computed_tokens=m.num_computed if align else None,
@@ -388,7 +388,7 @@ def disjoint_pools(args, timer, name):
         sp: list = []
         gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0], replay_cache=rec,
                               query_start_loc=m.query_start_loc, state_indices=m.state_indices, spec_query_len=Q,
-                              out=out, _collect=sp)
+                              out=out, state_cache_retain=STEP_STATE_RETAIN, _collect=sp)
         sp += list(ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
                                          block_table=m.block_table if align else None,
                                          num_computed_tokens=m.num_computed if align else None,
@@ -424,6 +424,89 @@ def disjoint_pools(args, timer, name):
             "frac": round(bytes_per_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "note": "the step on two batches with separate page pools taking turns (seeds 0 and 1): no step "
                     "finds the previous step's pages in a cache; only the step's own verify -> commit reuse is left"}
+
+
+def cold_step(args, timer, name):
+    """The step with nothing taken from a cache: two batches of the workload
+    with separate page pools (seeds 0 and 1) take turns, and before each
+    kernel a read sweep over a 512 MiB scratch buffer (twice the memory-side
+    cache, outside the kernel events) evicts what the previous kernels left,
+    so the commit finds none of its verify's pages cached. The verifies use
+    the library's default cache hint. The step's time is the sum of its two
+    kernels' event times."""
+    import torch
+
+    from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
+
+    dev = torch.device("cuda:0")
+    keep, specs = [], []
+    for seed in (0, 1):
+        w = W.make_workload(name, seed=seed, gen_device="cuda").to(dev)
+        s, m, inp = w.spec, w.meta, w.inputs[0]
+        B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+        align = m.block_table is not None
+        rec = ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=inp.k.dtype)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, [rec], spec_query_len=Q,
+                                                      max_num_reqs=B)
+        out = torch.empty(1, w.tokens, HV, V, dtype=inp.v.dtype, device=dev)
+        sp: list = []
+        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0], replay_cache=rec,
+                              query_start_loc=m.query_start_loc, state_indices=m.state_indices, spec_query_len=Q,
+                              out=out, _collect=sp)
+        sp += list(ctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc,
+                                         block_table=m.block_table if align else None,
+                                         num_computed_tokens=m.num_computed if align else None,
+                                         mamba_block_size=m.block_size if align else None, commit_conv=False))
+        assert [x.name for x in sp] == ["verify", "plan_fold"]
+        specs.append(sp)
+        keep.append((w, rec, ctx, out))
+    sweep = torch.ones(128 << 20, dtype=torch.float32, device=dev)  # 512 MiB, read by every sweep
+    sink = torch.empty((), dtype=torch.float32, device=dev)
+
+    def run(steps, marks=None):
+        for i in range(steps):
+            for j, sp in enumerate(specs[i % 2]):
+                torch.sum(sweep, dim=0, out=sink)
+                if marks:
+                    timer.record(marks[i][2 * j])
+                sp.launch()
+                if marks:
+                    timer.record(marks[i][2 * j + 1])
+
+    steps = max(2, args.steps - args.steps % 2)
+    run(max(2, min(args.warmup, 20)))
+    marks = [[timer.event() for _ in range(4)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    run(steps, marks)
+    torch.cuda.synchronize()
+    verify_us = sum(timer.elapsed(ev[0], ev[1]) for ev in marks) / steps * 1e3
+    fold_us = sum(timer.elapsed(ev[2], ev[3]) for ev in marks) / steps * 1e3
+    vb = cb = 0
+    for w, _, ctx, _ in keep:
+        nb = byte_model(w, ctx.commit_lens, ctx.final_state_indices, ctx.boundary_state_indices,
+                        ctx.boundary_recovery_lens)
+        vb += nb["verify"] / 2
+        cb += nb["commit"] / 2
+    del keep, specs, sweep
+    torch.cuda.empty_cache()
+
+    def rate(b, us):
+        return {"us": round(us, 2), "bytes": int(b), "gbs": round(b / (us * 1e-6) / 1e9, 1),
+                "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    from gdn_recoverssm_ascend import set_state_cache_retain
+
+    default_retain = set_state_cache_retain(0)
+    set_state_cache_retain(default_retain)
+    line = rate(vb + cb, verify_us + fold_us)
+    line["us_per_step"] = line.pop("us")
+    line["kernels"] = {"verify": rate(vb, verify_us), "plan_fold": rate(cb, fold_us)}
+    line["state_cache_retain"] = default_retain
+    line["note"] = ("two batches with separate page pools taking turns, a 512 MiB read sweep before every kernel "
+                    "(outside the events): every byte comes from HBM; us_per_step is the two kernels' event "
+                    "times; the verifies use the library's default cache hint")
+    return line
 
 
 def cpu_baseline(w_cpu, threads, budget_s=10.0):
@@ -474,6 +557,19 @@ def conv_bytes(spec, n, bnd, blen, num_pages, conv_dim, history, elem):
     return (int(active.sum()) * 2 + int(store_b.sum()) * 2) * conv_dim * history * elem
 
 
+# The single-layer step (one layer's verify, then its commit) re-reads the
+# verify's pages right away: its verifies read the last 256 MiB of their batch
+# (the MI355X memory-side cache) with ordinary loads, so the commit finds those
+# pages cached, and the rest non-temporally. Passed with every single-layer
+# verify below and named in the line's config; the library's own default is
+# the decode loop's (LOOP_STATE_RETAIN).
+STEP_STATE_RETAIN = 256 << 20
+
+# Cache groups of the decode loop committed through the grouped coordinator:
+# four groups of 12 layers, three to a bucket, so two buckets and the
+# publication across them.
+LOOP_GROUPS = 4
+
 # The decode loop's commit comes after all 48 layers' verifies, so nothing
 # re-reads a verify's pages from the memory-side cache; there the verify
 # itself runs fastest with the last quarter of a B=128 layer's 256 MiB read
@@ -483,30 +579,36 @@ def conv_bytes(spec, n, bnd, blen, num_pages, conv_dim, history, elem):
 LOOP_STATE_RETAIN = 64 << 20
 
 
-def run_decode_loop(name, *, deferred, steps=None, warmup=10):
-    """The decode loop with the verify cache hint set for it (restored after);
-    the retained bytes are reported in the line."""
-    from gdn_recoverssm_ascend import set_state_cache_retain
-
-    prev = set_state_cache_retain(LOOP_STATE_RETAIN)
-    try:
-        line = _run_decode_loop(name, deferred=deferred, steps=steps, warmup=warmup)
-    finally:
-        set_state_cache_retain(prev)
+def run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
+    """The decode loop; its verifies pass the loop's cache hint
+    (``LOOP_STATE_RETAIN``, the library's default), reported in the line."""
+    line = _run_decode_loop(name, deferred=deferred, steps=steps, warmup=warmup, groups=groups)
     line["state_cache_retain"] = LOOP_STATE_RETAIN
     return line
 
 
-def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
+def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
     """The decode-loop workload: every layer's verify, then one commit (plan,
     conv compaction, fold) across all layers, per speculative step, with the
     state carried from step to step (C += n, the source page becomes the final
     page) and fresh accepted lengths each step. With ``deferred`` each step runs
     the verify that applies the previous step's fold, then plan + conv.
-    Returns the loop's JSON line as a dict."""
+
+    ``groups=None`` commits through one ``GDNRecoverSSMCommitContext`` of all
+    layers. ``groups=k`` commits through ``GroupedCommitCoordinator``, the
+    commit the reference's commit proxy drives (layer_patch.py:108-149): the
+    layers form k cache groups of equal size on the same rows and block table,
+    three groups to a bucket, and an align step over several buckets ends with
+    the publication across them; deferred, ``commit_deferred`` plans, compacts
+    and publishes and the next verifies apply the folds (every committed row
+    continues on its final page, so nothing needs a ``settle``; its cost is
+    timed apart). Returns the loop's JSON line as a dict."""
+    from types import SimpleNamespace
+
     import torch
 
     from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.grouped_commit import GroupedCommitCoordinator
     from gdn_recoverssm_ascend.kernels import (
         GDNRecoverSSMCommitContext,
         ReplayRecordBuffers,
@@ -524,8 +626,6 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
     sets = 2 if deferred else 1
     recs = [[ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=w.inputs[0].k.dtype)
              for _ in range(L)] for _ in range(sets)]
-    ctxs = [GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, recs[i], spec_query_len=Q,
-                                                    max_num_reqs=B) for i in range(sets)]
     state_idx = m.state_indices.clone()
     computed = m.num_computed.clone()
     accepted = torch.zeros(B, dtype=torch.int32, device=dev)
@@ -534,15 +634,55 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
     outs = [torch.empty(1, w.tokens, HV, V, dtype=w.inputs[0].v.dtype, device=dev) for _ in range(L)]
     commit_kw = dict(block_table=m.block_table, num_computed_tokens=computed, mamba_block_size=m.block_size,
                      commit_conv=True)
-    cspecs, pendings = [], []
-    for i in range(sets):
-        specs_i: list = []
-        if deferred:
-            pendings.append(ctxs[i].commit_deferred(accepted, state_idx, m.query_start_loc, _collect=specs_i,
-                                                    **commit_kw))
-        else:
-            specs_i = list(ctxs[i].make_commit_specs(accepted, state_idx, m.query_start_loc, **commit_kw))
-        cspecs.append(specs_i)
+    coord = None
+    if groups is None:
+        ctxs = [GDNRecoverSSMCommitContext.from_tensors(w.conv_states, w.checkpoints, recs[i], spec_query_len=Q,
+                                                        max_num_reqs=B) for i in range(sets)]
+        cspecs, pendings = [], []
+        for i in range(sets):
+            specs_i: list = []
+            if deferred:
+                pendings.append(ctxs[i].commit_deferred(accepted, state_idx, m.query_start_loc, _collect=specs_i,
+                                                        **commit_kw))
+            else:
+                specs_i = list(ctxs[i].make_commit_specs(accepted, state_idx, m.query_start_loc, **commit_kw))
+            cspecs.append(specs_i)
+
+        def plan_arrays(i):
+            c = ctxs[i % sets]
+            return (c.commit_lens, c.final_state_indices, c.boundary_state_indices, c.boundary_recovery_lens)
+    else:
+        if L % groups:
+            raise ValueError(f"{L} layers do not split into {groups} equal cache groups")
+        per = L // groups
+        ctxs = [[GDNRecoverSSMCommitContext.from_tensors(w.conv_states[g * per:(g + 1) * per],
+                                                         w.checkpoints[g * per:(g + 1) * per],
+                                                         recs[i][g * per:(g + 1) * per], spec_query_len=Q,
+                                                         max_num_reqs=B) for g in range(groups)] for i in range(sets)]
+        payload = SimpleNamespace(state_indices=state_idx, query_start_loc=m.query_start_loc,
+                                  request_indices=m.request_indices.to(dev), block_table=m.block_table,
+                                  num_computed_tokens=computed, block_size=m.block_size,
+                                  request_rows=tuple(range(B)), query_lens=tuple([Q] * B))
+        metas = [[SimpleNamespace(recoverssm_commit=payload, recoverssm_builder=SimpleNamespace(),
+                                  recoverssm_context=c) for c in ctxs[i]] for i in range(sets)]
+        idx_mapping = m.idx_mapping.to(dev)
+        pcols = torch.full((B,), -1, dtype=torch.int32, device=dev)
+        pacc = torch.zeros(B, dtype=torch.int32, device=dev)
+        coord = GroupedCommitCoordinator()
+        deferred_step = []
+        for i in range(sets):
+            if deferred:
+                deferred_step.append(coord.commit_deferred(metas[i], accepted, idx_mapping, pcols, pacc))
+            else:
+                coord.commit(metas[i], accepted, idx_mapping, pcols, pacc)
+        buckets = list(coord._buckets.values()) + list(coord._previous.values())
+        first_bucket = [next(b for b in buckets if b.contexts[0] is ctxs[i][0]) for i in range(sets)]
+        pendings = [[p for g in range(groups) for p in deferred_step[i].pending(g)] for i in range(sets)] \
+            if deferred else []
+
+        def plan_arrays(i):
+            b = first_bucket[i % sets]
+            return (b.length, b.final, b.boundary, b.boundary_len)
     vspecs = []
     for i in range(sets):
         specs_i = []
@@ -555,13 +695,22 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
                 gdn_recoverssm_verify_deferred(inp.g, inp.beta, inp.q, inp.k, inp.v,
                                                pending=pendings[1 - i][layer], **kw)
             else:
-                gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, **kw)
+                gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, state_cache_retain=LOOP_STATE_RETAIN,
+                                      **kw)
         vspecs.append(specs_i)
     hist_lens = torch.empty(steps, 4, B, dtype=torch.int32, device=dev)
 
     def plan_of(i):
-        c = ctxs[i % sets]
-        return c.commit_lens[:B], c.final_state_indices[:B], c.boundary_state_indices[:B], c.boundary_recovery_lens[:B]
+        return tuple(t[:B] for t in plan_arrays(i))
+
+    def commit(i):
+        if coord is None:
+            for sp in cspecs[i % sets]:
+                sp.launch()
+        elif deferred:
+            coord.commit_deferred(metas[i % sets], accepted, idx_mapping, pcols, pacc)
+        else:
+            coord.commit(metas[i % sets], accepted, idx_mapping, pcols, pacc)
 
     def carry(i):
         lens_, fin_ = plan_of(i)[:2]
@@ -576,8 +725,7 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
             sp.launch()
         if marks:
             timer.record(marks[1])
-        for sp in cspecs[i % sets]:
-            sp.launch()
+        commit(i)
         if marks:
             timer.record(marks[2])
         if record is not None:
@@ -588,12 +736,13 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
     def restart():
         state_idx.copy_(start_idx)
         computed.copy_(start_c)
-        for c in ctxs:
-            c.commit_lens.zero_()  # no pending commit for the first deferred verify
+        # no pending commit for the first deferred verify
+        for lengths in ([plan_arrays(i)[0] for i in range(sets)] if coord is None else [b.length for b in buckets]):
+            lengths.zero_()
 
     stream = torch.cuda.current_stream(dev)
     timer = _HipTimer(stream.cuda_stream)
-    start_idx, start_c = state_idx.clone(), computed.clone()
+    start_idx, start_c = m.state_indices.clone(), m.num_computed.clone()
     restart()
     for i in range(warmup):
         step(steps + i)
@@ -617,6 +766,20 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
     torch.cuda.synchronize()
     verify_ms = sum(timer.elapsed(a, b) for a, b, _ in ev) / steps
     commit_ms = sum(timer.elapsed(b, c) for _, b, c in ev) / steps
+    settle_us = None
+    if coord is not None and deferred:
+        # Every row here continues on its final page, so no step needs a
+        # settle; a serving loop whose batch changes calls it (or flush(rows))
+        # before the verifies: its cost with nothing to fold, one fold launch
+        # per bucket over every row.
+        s0, s1 = timer.event(), timer.event()
+        torch.cuda.synchronize()
+        timer.record(s0)
+        for _ in range(5):
+            deferred_step[1].settle(metas[0])
+        timer.record(s1)
+        torch.cuda.synchronize()
+        settle_us = timer.elapsed(s0, s1) / 5 * 1e3
     lens, fin, bnd, blen = plan_of(0)
 
     nb = byte_model(w, lens, fin, bnd, blen)  # verify part is the same every step
@@ -652,12 +815,17 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": s.name, "layers": L, "rows": B, "key_heads": H, "value_heads": HV, "key_dim": K,
-                   "value_dim": V, "window": Q, "mode": "align", "block_size": m.block_size, "pages_per_layer": w.num_pages},
+                   "value_dim": V, "window": Q, "mode": "align", "block_size": m.block_size, "pages_per_layer": w.num_pages,
+                   "commit": "one context" if groups is None else f"coordinator, {groups} cache groups"},
         "phases_us_per_step": {"verify_all_layers": round(verify_ms * 1e3, 1), "commit": round(commit_ms * 1e3, 1)},
         "bytes_per_step": {"verify": verify_b, "commit": round(commit_b / steps), "conv": round(conv_b / steps)},
         "tokens_committed_per_step": round(tokens_committed / steps, 1),
         "mode": mode,
     }
+    if coord is not None:
+        line["launches_per_commit"] = coord.last_launch_count
+    if settle_us is not None:
+        line["settle_us"] = round(settle_us, 1)
     if deferred:
         # The step's state reads that the deferred commit removes: one page read
         # per committed (row, layer).
@@ -665,14 +833,16 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10):
         line["hbm_bytes_per_step"] = round((total_b - saved) / steps)
         line["hbm_gbs"] = round((total_b - saved) / (total_ms * 1e-3) / 1e9, 1)
         line["note"] = "value divides the ordinary flow's algorithmic bytes by this loop's time"
-    del w, recs, ctxs, outs, cspecs, vspecs, pendings
+    del w, recs, ctxs, outs, vspecs, pendings
+    coord = None
     torch.cuda.empty_cache()
     return line
 
 
 def decode_loop(args):
-    """--workload decode_loop_l48 [--deferred]: the loop's own JSON line."""
-    line = run_decode_loop(args.workload, deferred=args.deferred, steps=args.loop_steps, warmup=args.warmup)
+    """--workload decode_loop_l48 [--deferred] [--groups k]: the loop's own JSON line."""
+    line = run_decode_loop(args.workload, deferred=args.deferred, steps=args.loop_steps, warmup=args.warmup,
+                           groups=args.groups)
     print(json.dumps(line), flush=True)
     return 0
 
@@ -684,9 +854,16 @@ def decode_loop_summary(warmup):
     keys = ("us_per_step", "value", "hbm_frac", "steps", "warmup", "phases_us_per_step", "bytes_per_step",
             "tokens_committed_per_step")
     res = {}
-    for mode, deferred in (("ordinary", False), ("deferred", True)):
-        line = run_decode_loop("decode_loop_l48", deferred=deferred, warmup=warmup)
+    for mode, deferred, groups in (("ordinary", False, None), ("deferred", True, None),
+                                   ("coordinator_ordinary", False, LOOP_GROUPS),
+                                   ("coordinator_deferred", True, LOOP_GROUPS)):
+        line = run_decode_loop("decode_loop_l48", deferred=deferred, warmup=warmup, groups=groups)
         entry = {k: line[k] for k in keys}
+        if groups is not None:
+            entry["commit"] = line["config"]["commit"]
+            entry["launches_per_commit"] = line["launches_per_commit"]
+            if "settle_us" in line:
+                entry["settle_us"] = line["settle_us"]
         entry["gbs"] = entry.pop("value")
         if deferred:
             entry["equivalent_gbs"] = entry.pop("gbs")
@@ -699,7 +876,10 @@ def decode_loop_summary(warmup):
     res["note"] = ("gbs = algorithmic bytes of the whole loop (48 verifies, plan + fold, conv compaction per step) / "
                    "loop time; the deferred flow's equivalent_gbs divides the ordinary flow's bytes by its time; "
                    "the ordinary verifies retain the last state_cache_retain bytes of each layer's state "
-                   "(the deferred verify reads every row non-temporally)")
+                   "(the deferred verify reads every row non-temporally); coordinator_*: the same loop committed "
+                   f"through GroupedCommitCoordinator with the layers in {LOOP_GROUPS} cache groups (two buckets "
+                   "and the publication across them); no request leaves, so the deferred loop needs no settle "
+                   "(settle_us: one settle with nothing to fold)")
     return res
 
 
@@ -748,7 +928,7 @@ def main():
     verify_specs: list = []
     gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0], replay_cache=rec,
                           query_start_loc=m.query_start_loc, state_indices=m.state_indices, spec_query_len=Q, out=out,
-                          _collect=verify_specs)
+                          state_cache_retain=STEP_STATE_RETAIN, _collect=verify_specs)
     align_kw = dict(block_table=m.block_table if align else None,
                     num_computed_tokens=m.num_computed if align else None,
                     mamba_block_size=m.block_size if align else None)
@@ -832,7 +1012,7 @@ def main():
         gdn_recoverssm_verify_gated(a_raw, b_raw, inp.q, inp.k, inp.v, A_log=A_log, dt_bias=dt_bias,
                                     checkpoint_state=w.checkpoints[0], replay_cache=rec32,
                                     query_start_loc=m.query_start_loc, state_indices=m.state_indices,
-                                    spec_query_len=Q, out=out, _collect=gated_specs)
+                                    spec_query_len=Q, out=out, state_cache_retain=STEP_STATE_RETAIN, _collect=gated_specs)
 
         def alone(sp, reps=20):
             for _ in range(3):
@@ -930,6 +1110,7 @@ def main():
         ceiling = traffic_ceiling(w, nbytes, plan4, {k: v * 1e3 for k, v in kernel_ms.items()}, timer, args.steps)
     others = None if args.kernel_only else other_configs(args, timer, s.name)
     pools = None if args.kernel_only else disjoint_pools(args, timer, s.name)
+    cold = None if args.kernel_only else cold_step(args, timer, s.name)
     # The 48-layer decode loop at its own size (its own 10 warmup steps, after
     # which the carried state restarts from the seeded start).
     loop = None if args.kernel_only else decode_loop_summary(warmup=10)
@@ -945,7 +1126,7 @@ def main():
         pspecs: list = []
         gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[0],
                               replay_cache=prec, query_start_loc=m.query_start_loc, state_indices=m.state_indices,
-                              spec_query_len=Q, out=out, _collect=pspecs)
+                              spec_query_len=Q, out=out, state_cache_retain=STEP_STATE_RETAIN, _collect=pspecs)
         pspecs += list(pctx.make_commit_specs(m.accepted, m.state_indices, m.query_start_loc, commit_conv=False,
                                               **align_kw))
         for _ in range(args.warmup):
@@ -1055,6 +1236,7 @@ def main():
             "workload": s.name, "rows": B, "key_heads": H, "value_heads": HV, "key_dim": K, "value_dim": V,
             "window": Q, "mode": "align" if align else "none", "block_size": m.block_size,
             "state": "f32", "activations": "bf16", "key_records": "bf16",
+            "state_cache_retain": STEP_STATE_RETAIN,
         },
         "bytes": {**nbytes, "step": total},
         "kernels": per_kernel,
@@ -1067,6 +1249,7 @@ def main():
         "traffic_ceiling": ceiling,
         "other_configs": others,
         "disjoint_pools": pools,
+        "cold_step": cold,
         "decode_loop": loop,
     }
     print(json.dumps(line), flush=True)
