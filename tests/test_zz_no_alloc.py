@@ -7,7 +7,10 @@ copies of the same pages.
 Pages, conv states and the align publication must come out bit-identical (the
 two run the same kernels), on two calls in a row, the second with fewer rows:
 the library's plan buffer keeps the first call's contents, which the second
-must not read.
+must not read. Each single-context call is also checked against the CPU oracle
+directly (``oracle_plan_single``, ``oracle_fold``, ``oracle_conv_compact``):
+FP32 pages within max-abs 1e-5 relative to the pages' max-abs, pages outside
+the commit and conv histories bit-exact.
 """
 
 import ctypes
@@ -15,10 +18,11 @@ import ctypes
 import pytest
 import torch
 
+import gdn_oracle as O
 from gdn_recoverssm_ascend import _native as N
 from gdn_recoverssm_ascend.grouped_commit import GroupedCommitBucket
 from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext
-from test_gpu_commit import _entry, _group, _index_by_request, _to_dev
+from test_gpu_commit import HIST, _check_states, _entry, _group, _index_by_request, _planes, _to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -77,7 +81,67 @@ def test_single_context_two_calls(dev, align):
         ctx = GDNRecoverSSMCommitContext.from_tensors(gv, gc, gr, spec_query_len=4, max_num_reqs=32)
         _commit_noalloc(ctx.make_commit_specs(acc, src, qsl, **meta), dev)
         torch.cuda.synchronize()
-        _assert_same((rc, rv), (gc, gv), before, f"call {call} (B={B}, align={align})")
+        what = f"call {call} (B={B}, align={align})"
+        _assert_same((rc, rv), (gc, gv), before, what)
+        _assert_oracle(G, gc, gv, align, what)
+
+
+def _assert_oracle(G, pages, convs, align, what):
+    """The no-allocation commit's pages and conv states against the oracle."""
+    B = G["B"]
+    plan = O.oracle_plan_single(G["acc"], G["src"], G["qsl"], spec_query_len=4, num_blocks=G["NB"],
+                                block_table=G["table"], num_computed=G["C"], block_size=G["Bk"])
+    corrs, keys, decays = _planes(G)
+    want = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=G["src"], lengths=plan["commit_lens"],
+                         final=plan["final"], boundary=plan["boundary"], boundary_len=plan["boundary_len"],
+                         rows=B, num_blocks=G["NB"], record_rows=B)
+    _check_states(pages, want, torch.float32, set(plan["final"].tolist()) | set(plan["boundary"].tolist()))
+    want_conv = O.oracle_conv_compact(G["convs"], source=G["src"], lengths=plan["commit_lens"], final=plan["final"],
+                                      boundary=plan["boundary"], boundary_len=plan["boundary_len"], history=HIST,
+                                      num_blocks=G["NB"], rows=B, align=align)
+    for li, (got, w) in enumerate(zip(convs, want_conv)):
+        assert torch.equal(got.cpu(), w), f"{what}: layer {li} conv states differ from the oracle"
+    assert int(plan["commit_lens"].gt(0).sum()) > 0, f"{what}: nothing committed"
+
+
+def test_captured_commit_replays(dev):
+    """The no-allocation commit captured into a HIP graph (torch.cuda.graph)
+    after one eager call, then replayed three times on fresh copies of the
+    same pages, with eager copies and synchronisations between replays: every
+    replay's pages and conv states bit-identical to the eager call's."""
+    B = 16
+    G = _group(B, 2, 4, 128, 128, 4, 2, align=True, seed=333)
+    pages, convs, recs = _to_dev(G, dev)
+    fresh = [c.clone() for c in pages], [c.clone() for c in convs]
+    meta = dict(block_table=G["table"].to(dev), num_computed_tokens=G["C"].to(dev), mamba_block_size=G["Bk"])
+    acc, src, qsl = G["acc"].to(dev), G["src"].to(dev), G["qsl"].to(dev)
+    ctx = GDNRecoverSSMCommitContext.from_tensors(convs, pages, recs, spec_query_len=4, max_num_reqs=B)
+    specs = ctx.make_commit_specs(acc, src, qsl, **meta)
+
+    def reset():
+        for dst, s0 in zip(pages + convs, fresh[0] + fresh[1]):
+            dst.copy_(s0)
+
+    _commit_noalloc(specs, dev)  # eager: the reference result (and the buffer's address lookup)
+    torch.cuda.synchronize()
+    want = [c.clone() for c in pages], [c.clone() for c in convs]
+    _assert_oracle(G, want[0], want[1], True, "eager call")
+    reset()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _commit_noalloc(specs, dev)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(pages, fresh[0])), "capturing must not run the commit"
+    for replay in range(3):
+        reset()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for li, (a, b) in enumerate(zip(pages, want[0])):
+            assert torch.equal(a, b), f"replay {replay}: layer {li} pages differ from the eager call"
+        for li, (a, b) in enumerate(zip(convs, want[1])):
+            assert torch.equal(a, b), f"replay {replay}: layer {li} conv states differ from the eager call"
 
 
 def _bucket_commit(groups, dev, request_rows, sampled, mapping, noalloc):
