@@ -27,7 +27,8 @@ LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 # The source digest of a built library, written beside it by build().
 DIGEST_SUFFIX = ".digest"
 # Synthetic traffic probes for bench.py's measured ceilings (not part of the
-# verify / commit path): a library of their own.
+# verify / commit path): a library of their own, built by build_probe(), a
+# step apart from the product library's build().
 PROBE_SRC = os.path.join(CSRC_DIR, "probe", "traffic_probe.hip")
 PROBE_LIB_PATH = os.path.join(LIB_DIR, "libgdn_recoverssm_probe.so")
 ARCH = os.environ.get("GDN_OFFLOAD_ARCH", "gfx950")
@@ -74,9 +75,20 @@ def compile_flags() -> list[str]:
     ]
 
 
+def _compile(cc: str, src: str, obj: str, verbose: bool):
+    cmd = [cc, *compile_flags(), "-c", src, "-o", obj]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    text = r.stdout.decode(errors="replace")
+    text = "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l and l.strip() != "1 warning generated.")
+    return src, obj, r.returncode, text
+
+
 def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str:
-    """Compile every source (in parallel, largest first), link the shared
-    library and record the digest of the sources it was built from beside it."""
+    """Compile every library source (in parallel, largest first), link the
+    shared library and record the digest of the sources it was built from
+    beside it."""
     from concurrent.futures import ThreadPoolExecutor
 
     digest = source_digest()
@@ -87,18 +99,10 @@ def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str
     with tempfile.TemporaryDirectory(prefix="gdn_build_") as tmp:
 
         def compile_one(src):
-            obj = os.path.join(tmp, os.path.basename(src) + ".o")
-            cmd = [cc, *compile_flags(), "-c", src, "-o", obj]
-            if verbose:
-                print(" ".join(cmd), flush=True)
-            r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
-            text = r.stdout.decode(errors="replace")
-            text = "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l and l.strip() != "1 warning generated.")
-            return src, obj, r.returncode, text
+            return _compile(cc, src, os.path.join(tmp, os.path.basename(src) + ".o"), verbose)
 
         with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-            results = list(pool.map(compile_one, srcs + [PROBE_SRC]))
-        probe = results.pop()
+            results = list(pool.map(compile_one, srcs))
         errors = [f"{src}:\n{text}" for src, _, rc, text in results if rc != 0]
         if verbose:
             for src, _, rc, text in results:
@@ -113,16 +117,27 @@ def build(verbose: bool = False, jobs: int = min(8, os.cpu_count() or 1)) -> str
         if r.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + r.stdout.decode(errors="replace"))
         os.replace(tmp_lib, LIB_PATH)
-        if probe[2] != 0:
-            raise RuntimeError(f"hipcc failed:\n{probe[0]}:\n{probe[3]}")
-        r = subprocess.run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", probe[1], "-o", PROBE_LIB_PATH + ".tmp"],
+    with open(LIB_PATH + DIGEST_SUFFIX, "w") as f:
+        f.write(digest + "\n")
+    return LIB_PATH
+
+
+def build_probe(verbose: bool = False) -> str:
+    """The traffic probes bench.py times beside the kernels (synthetic
+    kernels moving each kernel's bytes in its access pattern): a library of
+    their own, which the verify / commit library does not need."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="gdn_probe_") as tmp:
+        src, obj, rc, text = _compile(cc, PROBE_SRC, os.path.join(tmp, "traffic_probe.o"), verbose)
+        if rc != 0:
+            raise RuntimeError(f"hipcc failed:\n{src}:\n{text}")
+        r = subprocess.run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", obj, "-o", PROBE_LIB_PATH + ".tmp"],
                            stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
         if r.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + r.stdout.decode(errors="replace"))
         os.replace(PROBE_LIB_PATH + ".tmp", PROBE_LIB_PATH)
-    with open(LIB_PATH + DIGEST_SUFFIX, "w") as f:
-        f.write(digest + "\n")
-    return LIB_PATH
+    return PROBE_LIB_PATH
 
 
 def built_digest(path: str) -> str | None:
@@ -135,5 +150,5 @@ def built_digest(path: str) -> str | None:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
-    print(path)
+    print(build(verbose="-v" in sys.argv))
+    print(build_probe(verbose="-v" in sys.argv))
