@@ -168,45 +168,39 @@ def measured_traffic(workload, kernel):
     return k["hbm_bytes"], os.path.relpath(path, HERE)
 
 
-def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
-    """Synthetic twins of the step's two kernels (csrc/probe/traffic_probe.hip):
-    the verify's state tiles, small reads and output / record writes, and the
-    fold's tile copies (source page -> final and boundary pages, written into a
-    scratch pool with the workload's page layout), moved in each kernel's own
-    access pattern with no arithmetic, timed as a step (verify twin, then fold
-    twin, an event between them) as the kernels are. The twin's time is what
-    the memory system sustains for that traffic; kernel_over_twin is the
-    kernel's time over it."""
+def _probe_lib():
     import ctypes
-
-    import torch
 
     from gdn_recoverssm_ascend import _build
 
     if not os.path.exists(_build.PROBE_LIB_PATH):
-        return {"note": f"{_build.PROBE_LIB_PATH} not built"}
+        return None
     lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     lib.gdn_probe_verify_twin.argtypes = [vp, vp, i64, vp, i64, vp, i64, vp, i64, vp]
     lib.gdn_probe_fold_twin.argtypes = [vp, vp, vp, vp, vp, i64, vp]
+    return lib
+
+
+def _verify_twin(lib, w, layer, nbytes, retain):
+    """The verify twin of one layer's launch: its state tiles (the rows before
+    the last ``retain`` bytes non-temporally in row runs, the rest in the
+    operand layout, as the verify reads them), its small reads and its output
+    and record writes. Returns (launch, launch without the small traffic,
+    bytes moved, tiles)."""
+    import torch
+
     s = w.spec
     B, HV, H, K, V = s.rows, s.value_heads, s.key_heads, s.key_dim, s.value_dim
-    if (K, V) != (128, 128) or w.checkpoints[0].dtype != torch.float32:
-        return {"note": "the twins model 64 KiB FP32 tiles (K = V = 128)"}
-    dev = w.checkpoints[0].device
-    ck = w.checkpoints[0]
+    ck = w.checkpoints[layer]
+    dev = ck.device
     tile = V * K * 4
     page_b, head_b = ck.stride(0) * 4, ck.stride(1) * 4
     idx = w.meta.state_indices.cpu().long()
     valid = (idx > 0) & (idx < w.num_pages)
-    rows = idx[valid]
     hv = torch.arange(HV)
-    tiles = (rows[:, None] * page_b + hv[None, :] * head_b).reshape(-1).to(dev)
+    tiles = (idx[valid][:, None] * page_b + hv[None, :] * head_b).reshape(-1).to(dev)
     n_v = tiles.numel()
-    # The verify reads the rows before the last `retain` bytes of state
-    # non-temporally (row runs) and the rest in the operand layout; the twin
-    # does the same for the same tiles.
-    retain = STEP_STATE_RETAIN
     keep_rows = -(-retain // (HV * V * K * 4))
     nt_rows = max(0, B - keep_rows)
     nt_tiles = int(valid[:nt_rows].sum()) * HV
@@ -218,6 +212,42 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     small_buf = torch.zeros(((n_v + 1) // 2) * small_dw + 1, dtype=torch.float32, device=dev)
     wbuf = torch.empty(n_v * write_dw + 1, dtype=torch.float32, device=dev)
     sink = torch.empty(n_v, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run(sdw=small_dw, wdw=write_dw):
+        st = lib.gdn_probe_verify_twin(ck.data_ptr(), tiles.data_ptr(), n_v, small_buf.data_ptr(), sdw,
+                                       wbuf.data_ptr(), wdw, sink.data_ptr(), nt_tiles, stream)
+        assert st == 0, f"verify twin: status {st}"
+
+    run.keep = (tiles, small_buf, wbuf, sink)
+    v_bytes = n_v * tile + ((n_v + 1) // 2) * small_dw * 4 + n_v * write_dw * 4
+    return run, (lambda: run(0, 0)), v_bytes, n_v
+
+
+def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps, retain=None):
+    """Synthetic twins of the step's two kernels (csrc/probe/traffic_probe.hip):
+    the verify's state tiles, small reads and output / record writes, and the
+    fold's tile copies (source page -> final and boundary pages, written into a
+    scratch pool with the workload's page layout), moved in each kernel's own
+    access pattern with no arithmetic, timed as a step (verify twin, then fold
+    twin, an event between them) as the kernels are. The twin's time is what
+    the memory system sustains for that traffic; kernel_over_twin is the
+    kernel's time over it."""
+    import torch
+
+    lib = _probe_lib()
+    if lib is None:
+        return {"note": "the traffic probe library is not built"}
+    s = w.spec
+    B, HV, K, V = s.rows, s.value_heads, s.key_dim, s.value_dim
+    if (K, V) != (128, 128) or w.checkpoints[0].dtype != torch.float32:
+        return {"note": "the twins model 64 KiB FP32 tiles (K = V = 128)"}
+    dev = w.checkpoints[0].device
+    ck = w.checkpoints[0]
+    tile = V * K * 4
+    page_b, head_b = ck.stride(0) * 4, ck.stride(1) * 4
+    hv = torch.arange(HV)
+    vtwin, vtwin_reads, v_bytes, n_v = _verify_twin(lib, w, 0, nbytes, STEP_STATE_RETAIN if retain is None else retain)
     n, fin, bnd, blen = (t.cpu().long()[:B] for t in plan)
     src = w.meta.state_indices.cpu().long()
     act = n > 0
@@ -230,11 +260,6 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     n_f = so.numel()
     pool = torch.empty_like(ck)
     stream = torch.cuda.current_stream(dev).cuda_stream
-
-    def vtwin(sdw=small_dw, wdw=write_dw):
-        st = lib.gdn_probe_verify_twin(ck.data_ptr(), tiles.data_ptr(), n_v, small_buf.data_ptr(), sdw,
-                                       wbuf.data_ptr(), wdw, sink.data_ptr(), nt_tiles, stream)
-        assert st == 0, f"verify twin: status {st}"
 
     def ftwin():
         st = lib.gdn_probe_fold_twin(ck.data_ptr(), pool.data_ptr(), so.data_ptr(), do.data_ptr(), d2.data_ptr(),
@@ -257,18 +282,17 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
     f_us = sum(timer.elapsed(ev[1], ev[2]) for ev in marks) / steps * 1e3
     r0, r1 = timer.event(), timer.event()
     for _ in range(3):
-        vtwin(0, 0)
+        vtwin_reads()
     torch.cuda.synchronize()
     timer.record(r0)
     for _ in range(steps):
-        vtwin(0, 0)
+        vtwin_reads()
     timer.record(r1)
     torch.cuda.synchronize()
     ro_us = timer.elapsed(r0, r1) / steps * 1e3
-    v_bytes = n_v * tile + ((n_v + 1) // 2) * small_dw * 4 + n_v * write_dw * 4
     f_bytes = n_f * tile * 2 + int(d2.ge(0).sum()) * tile
     torch.cuda.synchronize()
-    del pool, wbuf, small_buf
+    del pool, vtwin
     torch.cuda.empty_cache()
     return {
         "verify_twin": {"us": round(v_us, 2), "bytes": v_bytes, "gbs": round(v_bytes / (v_us * 1e-6) / 1e9, 1),
@@ -285,6 +309,65 @@ def traffic_ceiling(w, nbytes, plan, kernel_us, timer, steps):
                 "reads_only: the verify twin without its small reads and writes; the verify twin reads the tiles "
                 "of the rows before the last retained bytes non-temporally in row runs, as the verify does",
     }
+
+
+def loop_verify_ceiling(timer, reps=10, layers=6):
+    """The decode loop's verify against its twin, both as the loop runs them:
+    one launch per layer, back to back over `layers` layers of the loop's
+    workload (B=128, each layer's own page pool), the loop's cache hint. The
+    twin of each layer moves that launch's bytes in the verify's access
+    pattern with no arithmetic."""
+    import torch
+
+    from gdn_recoverssm_ascend import workloads as W
+    from gdn_recoverssm_ascend.kernels import ReplayRecordBuffers, gdn_recoverssm_verify
+
+    lib = _probe_lib()
+    if lib is None:
+        return {"note": "the traffic probe library is not built"}
+    dev = torch.device("cuda:0")
+    w = W.make_workload("decode_loop_l48", layers=layers, gen_device="cuda").to(dev)
+    s, m = w.spec, w.meta
+    B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
+    recs = [ReplayRecordBuffers.allocate(B, HV, H, Q, V, K, device=dev, key_dtype=w.inputs[0].k.dtype)
+            for _ in range(layers)]
+    specs = []
+    for layer in range(layers):
+        inp = w.inputs[layer]
+        gdn_recoverssm_verify(inp.g, inp.beta, inp.q, inp.k, inp.v, checkpoint_state=w.checkpoints[layer],
+                              replay_cache=recs[layer], query_start_loc=m.query_start_loc,
+                              state_indices=m.state_indices, spec_query_len=Q, state_cache_retain=LOOP_STATE_RETAIN,
+                              _collect=specs)
+    nb = byte_model(w, torch.zeros(B, dtype=torch.int32), m.state_indices, m.state_indices,
+                    torch.zeros(B, dtype=torch.int32))
+    twins = [_verify_twin(lib, w, layer, nb, LOOP_STATE_RETAIN) for layer in range(layers)]
+
+    def timed(fns):
+        for _ in range(3):
+            for f in fns:
+                f()
+        e0, e1 = timer.event(), timer.event()
+        torch.cuda.synchronize()
+        timer.record(e0)
+        for _ in range(reps):
+            for f in fns:
+                f()
+        timer.record(e1)
+        torch.cuda.synchronize()
+        return timer.elapsed(e0, e1) / (reps * len(fns)) * 1e3
+
+    k_us = timed([sp.launch for sp in specs])
+    t_us = timed([t[0] for t in twins])
+    r_us = timed([t[1] for t in twins])
+    vb = nb["verify"]
+    del w, recs, specs, twins
+    torch.cuda.empty_cache()
+    return {"kernel_us": round(k_us, 2), "twin_us": round(t_us, 2), "reads_only_us": round(r_us, 2),
+            "bytes": vb, "kernel_frac": round(vb / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "twin_frac": round(vb / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_over_twin": round(k_us / t_us, 3), "layers_back_to_back": layers,
+            "note": "one B=128 layer's verify as the decode loop runs it (launches back to back over several "
+                    "layers' pools, 64 MiB retained) against its traffic twin timed the same way"}
 
 
 def kernel_times(specs, timer, steps):
@@ -871,6 +954,9 @@ def decode_loop_summary(warmup):
             entry["hbm_bytes_per_step"] = line["hbm_bytes_per_step"]
             entry["hbm_gbs"] = line["hbm_gbs"]
         res[mode] = entry
+    import torch
+
+    res["verify_ceiling"] = loop_verify_ceiling(_HipTimer(torch.cuda.current_stream().cuda_stream))
     res["config"] = run_decode_loop_config()
     res["state_cache_retain"] = LOOP_STATE_RETAIN
     res["note"] = ("gbs = algorithmic bytes of the whole loop (48 verifies, plan + fold, conv compaction per step) / "

@@ -74,6 +74,21 @@ __device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int voff,
 constexpr int kRecPasses = 4;  // workgroup passes per batch of record loads
 constexpr int64_t kEarlyMaxGrid = 4096;
 
+// PACED: in launches of many rounds of workgroups (a commit over every layer
+// of a model: 48 layers x 128 rows x 32 heads is ~200k workgroups on 768
+// slots) each workgroup waits ~2.5 us (s_sleep 96: 64 x 96 cycles) before its
+// state loads. The launch then sustains more bandwidth: the 48-layer commit
+// of the decode loop took 3.61-3.63 ms with the wait against 3.76-3.77 ms
+// without it, and a workgroup whose planning took one more dependent load (a
+// request mapping) gained the same. Fewer workgroups have their 64 KiB load
+// bursts queued at once. A launch of a few rounds (a single layer's commit,
+// ~8000 workgroups) keeps the immediate order, where each workgroup's latency
+// shows (at B=256 one more dependent load before the state loads took the
+// plan + fold from 146 to 148.5 us).
+constexpr int64_t kPacedMinGrid = 32768;
+constexpr int kPaceSleep = 96;
+enum FoldOrder : int { kOrderDefault = 0, kOrderEarly = 1, kOrderPaced = 2 };
+
 // The per-layer words a workgroup needs before its first state load: the
 // layer's plan group and its tile and record tables (state_addrs, state_bs,
 // corr_addrs, corr_bs, key_addrs, key_bs, decay_addrs, decay_bs at the layer).
@@ -120,10 +135,11 @@ __device__ __forceinline__ LayerRefs layer_refs_load(const FoldArgs &a, int64_t 
   return L;
 }
 
-template <typename S, typename KT, bool PLANNED, bool EARLY>
+template <typename S, typename KT, bool PLANNED, int ORDER>
 __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, int64_t w) {
   constexpr int E = Chunk<S>::E;
   constexpr int ITERS = 64 / E;  // chunks held per thread per batch (64 f32 values)
+  constexpr bool EARLY = ORDER == kOrderEarly;
   extern __shared__ float lds[];
 
   // 32-bit division: the grid is below 2^31 workgroups (checked on the host),
@@ -218,6 +234,7 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   };
   float rec_c[kRecPasses], rec_k[kRecPasses];
   if constexpr (EARLY) load_records(0, rec_c, rec_k);
+  if constexpr (ORDER == kOrderPaced) __builtin_amdgcn_s_sleep(kPaceSleep);
   // Issue the first batch of state loads before staging the records.
   uint4 raw[ITERS];
 #pragma unroll
@@ -305,15 +322,15 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
   }
 }
 
-template <typename S, typename KT, bool EARLY>
+template <typename S, typename KT, int ORDER>
 __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
   warm_kernel_args<int(sizeof(FoldArgs))>();
-  fold_body<S, KT, false, EARLY>(a, nullptr, blockIdx.x);
+  fold_body<S, KT, false, ORDER>(a, nullptr, blockIdx.x);
 }
 
 // The first `writers` workgroups store the plan (one thread per row); the rest
 // fold, each planning its own row.
-template <typename S, typename KT, bool EARLY>
+template <typename S, typename KT, int ORDER>
 __global__ __launch_bounds__(kFoldThreads) void plan_fold_kernel(FoldArgs a, PlanArgs p, int64_t writers) {
   warm_kernel_args<int(sizeof(FoldArgs) + sizeof(PlanArgs) + sizeof(int64_t))>();
   const int64_t w = blockIdx.x;
@@ -322,17 +339,17 @@ __global__ __launch_bounds__(kFoldThreads) void plan_fold_kernel(FoldArgs a, Pla
     if (row < p.rows) plan_write_row(p, row);
     return;
   }
-  fold_body<S, KT, true, EARLY>(a, &p, w - writers);
+  fold_body<S, KT, true, ORDER>(a, &p, w - writers);
 }
 
-template <typename S, bool EARLY>
+template <typename S, int ORDER>
 static void launch_fold_key(int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a,
                             const PlanArgs *plan, int64_t writers) {
 #define GDN_FOLD_LAUNCH(KT)                                                                                   \
   if (plan)                                                                                                   \
-    hipLaunchKernelGGL((plan_fold_kernel<S, KT, EARLY>), grid, dim3(kFoldThreads), lds, s, a, *plan, writers); \
+    hipLaunchKernelGGL((plan_fold_kernel<S, KT, ORDER>), grid, dim3(kFoldThreads), lds, s, a, *plan, writers); \
   else                                                                                                        \
-    hipLaunchKernelGGL((fold_kernel<S, KT, EARLY>), grid, dim3(kFoldThreads), lds, s, a);
+    hipLaunchKernelGGL((fold_kernel<S, KT, ORDER>), grid, dim3(kFoldThreads), lds, s, a);
   switch (key_dtype) {
     case GDN_DT_BF16: GDN_FOLD_LAUNCH(bf16) break;
     case GDN_DT_F16: GDN_FOLD_LAUNCH(f16) break;
@@ -342,12 +359,13 @@ static void launch_fold_key(int key_dtype, dim3 grid, size_t lds, hipStream_t s,
 }
 
 template <typename S>
-static void launch_fold_state(bool early, int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a,
+static void launch_fold_state(int order, int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a,
                               const PlanArgs *plan, int64_t writers) {
-  if (early)
-    launch_fold_key<S, true>(key_dtype, grid, lds, s, a, plan, writers);
-  else
-    launch_fold_key<S, false>(key_dtype, grid, lds, s, a, plan, writers);
+  switch (order) {
+    case kOrderEarly: launch_fold_key<S, kOrderEarly>(key_dtype, grid, lds, s, a, plan, writers); break;
+    case kOrderPaced: launch_fold_key<S, kOrderPaced>(key_dtype, grid, lds, s, a, plan, writers); break;
+    default: launch_fold_key<S, kOrderDefault>(key_dtype, grid, lds, s, a, plan, writers); break;
+  }
 }
 
 static bool float_dtype_ok(int32_t dt) { return dt == GDN_DT_F32 || dt == GDN_DT_BF16 || dt == GDN_DT_F16; }
@@ -466,10 +484,11 @@ static int launch_fold(const gdn_fold_ext *ext, int64_t grid, size_t lds, const 
   // (make_fold_args has checked that every window's records fit 32-bit offsets.)
   const bool early = grid <= kEarlyMaxGrid && a.Q * a.V <= kRecPasses * kFoldThreads &&
                      a.Q * a.KP <= kRecPasses * kFoldThreads;
+  const int order = early ? kOrderEarly : grid > kPacedMinGrid ? kOrderPaced : kOrderDefault;
   switch (ext->state_dtype) {
-    case GDN_DT_BF16: launch_fold_state<bf16>(early, ext->key_dtype, g, lds, s, a, plan, writers); break;
-    case GDN_DT_F16: launch_fold_state<f16>(early, ext->key_dtype, g, lds, s, a, plan, writers); break;
-    default: launch_fold_state<float>(early, ext->key_dtype, g, lds, s, a, plan, writers); break;
+    case GDN_DT_BF16: launch_fold_state<bf16>(order, ext->key_dtype, g, lds, s, a, plan, writers); break;
+    case GDN_DT_F16: launch_fold_state<f16>(order, ext->key_dtype, g, lds, s, a, plan, writers); break;
+    default: launch_fold_state<float>(order, ext->key_dtype, g, lds, s, a, plan, writers); break;
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {

@@ -443,6 +443,80 @@ def test_batch_change_with_flush(dev):
         _check_verify(outs[layer], recs[1][layer], r1, f"step 1 layer {layer}")
 
 
+def test_settle_folds_what_the_verify_does_not_apply(dev):
+    """``settle_deferred`` decides on the device which pending rows the next
+    verify will not apply and folds exactly those: here two departed requests
+    (one whose commit writes a boundary snapshot) and a continued request
+    whose next state index names another page than its pending final page.
+    The verify then applies the rest. Every page equals the oracle's fold of
+    step 0 (each commit folded once), and step 1's outputs equal the oracle's
+    verify from those pages, the moved request's from its new, unfolded page."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=41)
+    s = w.spec
+    L, B, Q = s.layers, s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[::3] = 2
+    st = _first_step(w, dev, acc)
+    plan = st["plan"]
+    n, fin, bnd = plan["commit_lens"], plan["final"], plan["boundary"]
+    pad = int(w.extras["padded_rows"][0])
+    crossing = [r for r in range(B) if int(n[r]) > 0 and int(bnd[r]) > 0 and int(bnd[r]) != int(fin[r])]
+    plain = [r for r in range(B) if int(n[r]) > 0 and r not in crossing]
+    assert crossing and len(plain) > 1, "the seed must give a crossing and two plain commits"
+    leaving = [crossing[0], plain[0]]
+    moved = plain[1]
+    gen = torch.Generator().manual_seed(44)
+    stay = [r for r in range(B) if r not in leaving and r != pad]
+    stay = [stay[i] for i in torch.randperm(len(stay), generator=gen).tolist()]
+    new_request = 1000
+    next_requests = stay[:3] + [new_request] + stay[3:]
+    B1 = len(next_requests)
+    src_col = w.extras["source_col"]
+    table = w.meta.block_table
+    new_page = int(table[pad, src_col[pad]])
+    moved_page = int(table[pad, src_col[pad] + 1])  # the padded row's next page: no row uses it
+    assert moved_page > 0 and moved_page != new_page
+
+    def next_index(r):
+        if r == new_request:
+            return new_page
+        if r == moved:
+            return moved_page
+        return int(fin[r]) if int(n[r]) > 0 else int(w.meta.state_indices[r])
+
+    idx1 = torch.tensor([next_index(r) for r in next_requests], dtype=torch.int32)
+    qsl1 = torch.arange(B1 + 1, dtype=torch.int32) * Q
+    inputs1 = [W.make_layer_inputs(s, B1 * Q, gen) for _ in range(L)]
+    pending1, left = continue_pending(st["pending"], list(range(B)), next_requests)
+    assert left == sorted(leaving + [pad])
+    ckpts, recs, ctx = st["ckpts"], st["recs"], st["ctx"]
+    qd, idx_d = qsl1.to(dev), idx1.to(dev)
+    before = [c.cpu() for c in w.checkpoints]
+    ctx.settle_deferred(idx_d, pending1[0].rows)
+    torch.cuda.synchronize()
+    settled = torch.tensor([1 if r in leaving or r == moved else 0 for r in range(B)], dtype=torch.int32)
+    part = _oracle_fold(before, st["results"], plan, B, w.num_pages, lengths=plan["commit_lens"] * settled)
+    touched_part = _touched({**plan, "commit_lens": plan["commit_lens"] * settled}, B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], part[layer], touched_part, f"layer {layer}: pages after the settle")
+    outs = []
+    for layer in range(L):
+        i = inputs1[layer]
+        outs.append(gdn_recoverssm_verify_deferred(
+            i.g.to(dev), i.beta.to(dev), i.q.to(dev), i.k.to(dev), i.v.to(dev), checkpoint_state=ckpts[layer],
+            replay_cache=recs[1][layer], pending=pending1[layer], query_start_loc=qd, state_indices=idx_d,
+            spec_query_len=Q))
+    torch.cuda.synchronize()
+    want = _oracle_fold(before, st["results"], plan, B, w.num_pages)
+    touched = _touched(plan, B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after settle + verify")
+        i = inputs1[layer]
+        r1 = O.oracle_verify(i.q, i.k, i.v, i.g, i.beta, want[layer], qsl1, idx1, Q)
+        _check_verify(outs[layer], recs[1][layer], r1, f"step 1 layer {layer}")
+
+
 def test_rows_past_the_pending_plan_do_not_apply(dev):
     """The pending plan covers `num_rows` rows, and plan entries past them
     (here: the rest of a full plan, as an older, larger step leaves them)
