@@ -81,6 +81,9 @@ __global__ __launch_bounds__(256) void conv_compact_kernel(
     blen = boundary_lens[plan_row];
     store_b = bidx > null_block && bidx < num_blocks && blen >= 1 && blen - 1 + history <= window;
   }
+  // One accepted token kept on its own page: the history already starts at
+  // position 0 of the window, so the copy would rewrite every byte unchanged.
+  if (n == 1 && fin == src && !store_b) return;
   E *base = reinterpret_cast<E *>(addrs[layer]);
   const int64_t bs = block_strides[layer], ds = dim_strides[layer], ts = token_strides[layer];
   const int64_t c0 = tile * (kConvChannelsPerThread * 256) + threadIdx.x;
