@@ -26,7 +26,7 @@ from . import _native as N
 from ._rules import enforce, fail, require
 from ._tables import LayerPages
 from .kernels import (_FOLD_LENGTHS_ARG, NULL_BLOCK_ID, PendingCommit, _conv_spec, _fill_plan_group,
-                      _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _unapplied_lengths)
+                      _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _unapplied_lengths, _request_row_map)
 
 logger = logging.getLogger("gdn_recoverssm_ascend.grouped_commit")
 
@@ -324,18 +324,8 @@ class DeferredGroupedCommit:
         pending row r, ``next_requests[b]`` that of next row b. Returns the
         sorted pending rows whose request left; ``settle`` or ``flush`` must
         fold them."""
-        require(len(previous_requests) >= self.num_rows, "previous request ids do not cover the pending rows")
-        where = {}
-        for r, req in enumerate(previous_requests[:self.num_rows]):
-            require(req not in where, f"request {req!r} appears twice in the pending step")
-            where[req] = r
-        seen, mapping = set(), []
-        for req in next_requests:
-            require(req not in seen, f"request {req!r} appears twice in the next batch")
-            seen.add(req)
-            mapping.append(where.get(req, -1))
-        self.rows = torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=self.rows.device)
-        return sorted(r for req, r in where.items() if req not in seen)
+        self.rows, left = _request_row_map(self.num_rows, previous_requests, next_requests, self.rows.device)
+        return left
 
     def _fold(self, bucket, fold, lengths) -> None:
         args = list(fold.args)

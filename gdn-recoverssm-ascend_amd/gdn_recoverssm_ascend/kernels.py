@@ -503,6 +503,17 @@ def continue_pending(pending: Sequence[PendingCommit], previous_requests: Sequen
     require(len(pending) > 0, "no pending commits to continue")
     num_rows = int(pending[0].num_rows)
     require(all(int(p.num_rows) == num_rows for p in pending), "pending commits of one step disagree on their rows")
+    rows, left = _request_row_map(num_rows, previous_requests, next_requests, pending[0].rows.device)
+    return tuple(replace(p, rows=rows) for p in pending), left
+
+
+def _request_row_map(num_rows: int, previous_requests: Sequence, next_requests: Sequence, device):
+    """The row map of a deferred step's next batch, keyed by request:
+    ``previous_requests[r]`` is the request of pending row r (r < num_rows),
+    ``next_requests[b]`` that of next row b. Returns (int32 tensor on
+    ``device``: next row -> pending row of the same request, -1 for a new
+    request; a single -1 for an empty batch, which the kernels never index)
+    and the sorted pending rows whose request is not in the next batch."""
     require(len(previous_requests) >= num_rows, "previous request ids do not cover the pending rows")
     where = {}
     for r, req in enumerate(previous_requests[:num_rows]):
@@ -515,8 +526,7 @@ def continue_pending(pending: Sequence[PendingCommit], previous_requests: Sequen
         seen.add(req)
         mapping.append(where.get(req, -1))
     left = sorted(r for req, r in where.items() if req not in seen)
-    rows = torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=pending[0].rows.device)
-    return tuple(replace(p, rows=rows) for p in pending), left
+    return torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=device), left
 
 
 _PENDING_RULES = (
