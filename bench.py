@@ -1026,7 +1026,9 @@ def decode_loop_summary(warmup):
     res["config"] = run_decode_loop_config()
     res["state_cache_retain"] = LOOP_STATE_RETAIN
     res["note"] = ("gbs = algorithmic bytes of the whole loop (48 verifies, plan + fold, conv compaction per step) / "
-                   "loop time; the deferred flow's equivalent_gbs divides the ordinary flow's bytes by its time; "
+                   "loop time; each step's scheduler inputs (accepted lengths, state indices, computed tokens) "
+                   "are recorded by a first pass that carries the state and are in place before the timed "
+                   "region; the deferred flow's equivalent_gbs divides the ordinary flow's bytes by its time; "
                    "the ordinary verifies retain the last state_cache_retain bytes of each layer's state "
                    "(the deferred verify reads every row non-temporally); coordinator_*: the same loop committed "
                    f"through GroupedCommitCoordinator with the layers in {LOOP_GROUPS} cache groups (two buckets "
