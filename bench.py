@@ -831,6 +831,7 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
         meta_si.append(state_idx.clone())
         meta_c.append(computed.clone())
         carried_step(i)
+    end_si, end_c = state_idx.clone(), computed.clone()  # the metadata after the last step
     torch.cuda.synchronize()
 
     def bind_step(i):
@@ -913,13 +914,17 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
     torch.cuda.synchronize()
     verify_ms = sum(timer.elapsed(a, b) for a, b, _ in ev) / steps
     commit_ms = sum(timer.elapsed(b, c) for _, b, c in ev) / steps
-    settle_us = None
+    settle_us = flush_us = None
     if coord is not None and deferred:
         # Every row here continues on its final page, so no step needs a
         # settle; a serving loop whose batch changes calls it (or flush(rows))
         # before the verifies: its cost with nothing to fold, one fold launch
         # per bucket over every row.
-        # The first call loads its kernels; timed are the calls after it.
+        # The next step's metadata (the last step's carried forward): every
+        # pending row continues on its final page. The first call loads its
+        # kernels; timed are the calls after it.
+        state_idx.copy_(end_si)
+        computed.copy_(end_c)
         deferred_step[1].settle(metas[0])
         s0, s1 = timer.event(), timer.event()
         torch.cuda.synchronize()
@@ -929,6 +934,17 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
         timer.record(s1)
         torch.cuda.synchronize()
         settle_us = timer.elapsed(s0, s1) / 5 * 1e3
+        # What a step whose batch lost two requests pays instead: their
+        # pending commits folded through the fold's row list (timing only:
+        # the same two rows folded again each call).
+        deferred_step[1].flush(rows=[0, 1])
+        torch.cuda.synchronize()
+        timer.record(s0)
+        for _ in range(5):
+            deferred_step[1].flush(rows=[0, 1])
+        timer.record(s1)
+        torch.cuda.synchronize()
+        flush_us = timer.elapsed(s0, s1) / 5 * 1e3
     lens, fin, bnd, blen = plan_of(0)
 
     nb = byte_model(w, lens, fin, bnd, blen)  # verify part is the same every step
@@ -975,6 +991,7 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
         line["launches_per_commit"] = coord.last_launch_count
     if settle_us is not None:
         line["settle_us"] = round(settle_us, 1)
+        line["flush_two_rows_us"] = round(flush_us, 1)
     if deferred:
         # The step's state reads that the deferred commit removes: one page read
         # per committed (row, layer).
@@ -1013,6 +1030,7 @@ def decode_loop_summary(warmup):
             entry["launches_per_commit"] = line["launches_per_commit"]
             if "settle_us" in line:
                 entry["settle_us"] = line["settle_us"]
+                entry["flush_two_rows_us"] = line["flush_two_rows_us"]
         entry["gbs"] = entry.pop("value")
         if deferred:
             entry["equivalent_gbs"] = entry.pop("gbs")
@@ -1033,7 +1051,9 @@ def decode_loop_summary(warmup):
                    "(the deferred verify reads every row non-temporally); coordinator_*: the same loop committed "
                    f"through GroupedCommitCoordinator with the layers in {LOOP_GROUPS} cache groups (two buckets "
                    "and the publication across them); no request leaves, so the deferred loop needs no settle "
-                   "(settle_us: one settle with nothing to fold)")
+                   "(settle_us: one settle with nothing to fold; flush_two_rows_us: the commits of two rows "
+                   "folded across every layer through the fold's row list, what a batch that loses two "
+                   "requests pays)")
     return res
 
 

@@ -87,6 +87,10 @@ extern "C" int gdn_recoverssm_commit_noalloc(const gdn_plan_launch *plan, void *
     set_error("commit_noalloc: tiling ABI expects %d config fields", GDN_FOLD_CONFIG_FIELDS);
     return GDN_ERR_INVALID;
   }
+  if (ext && ext->row_list) {
+    set_error("commit_noalloc: a row list applies to gdn_recoverssm_fold only");
+    return GDN_ERR_INVALID;
+  }
   const bool grouped = (plan->flags & GDN_PLAN_GROUPED) != 0;
   const gdn_plan_group &g0 = plan->groups[0];
   // The conv compaction reads the plan's source in a grouped commit and the

@@ -35,6 +35,10 @@ struct FoldArgs {
   int32_t kp_log, kch_log;  // KP and KCH are powers of two
   uint32_t v_magic;         // div16_magic(V)
   int32_t source_dtype;
+  // Plan rows to fold (unplanned fold only; NULL: rows 0..rows-1): the grid
+  // covers grid_rows = row_list_len entries instead of `rows`.
+  const int32_t *row_list;
+  int64_t grid_rows;
 };
 
 constexpr int kFoldThreads = 256;
@@ -144,10 +148,19 @@ __device__ __forceinline__ void fold_body(const FoldArgs &a, const PlanArgs *p, 
 
   // 32-bit division: the grid is below 2^31 workgroups (checked on the host),
   // and a 64-bit division here became a long inline sequence per index.
-  const uint32_t wu = uint32_t(w), heads = uint32_t(a.heads), rows = uint32_t(a.rows);
+  const uint32_t wu = uint32_t(w), heads = uint32_t(a.heads), rows = uint32_t(a.grid_rows);
   const int64_t hv = wu % heads;
-  const int64_t row = (wu / heads) % rows;
+  int64_t row = (wu / heads) % rows;
   const int64_t layer = wu / (heads * rows);
+  if constexpr (!PLANNED) {
+    if (a.row_list) {
+      // Listed rows: strictly increasing; an entry out of range or not above
+      // the one before it folds nothing (a repeated row is folded once).
+      const int64_t i = row;
+      row = a.row_list[i];
+      if (row < 0 || row >= a.rows || (i > 0 && a.row_list[i - 1] >= row)) return;
+    }
+  }
   int64_t src, fin, bidx;
   int n, blen;
   PlanRow pr;
@@ -466,8 +479,18 @@ static int make_fold_args(const int64_t *state_addrs, const int64_t *state_block
   a.kch_log = kch_log;
   a.kp_log = kch_log + (E == 8 ? 3 : E == 4 ? 2 : 1);
   a.v_magic = div16_magic(uint32_t(V));
+  a.grid_rows = rows;
+  if (ext->row_list) {
+    if (ext->row_list_len < 1 || ext->row_list_len > rows) {
+      set_error("fold: a row list of %lld entries for %lld rows (1..rows entries)", (long long)ext->row_list_len,
+                (long long)rows);
+      return GDN_ERR_INVALID;
+    }
+    a.row_list = ext->row_list;
+    a.grid_rows = ext->row_list_len;
+  }
   *out = a;
-  *grid = layers * rows * heads;
+  *grid = layers * a.grid_rows * heads;
   *lds = size_t(query_len) * size_t(V + a.KP) * sizeof(float);
   return GDN_OK;
 }
@@ -562,6 +585,10 @@ extern "C" int gdn_recoverssm_plan_fold(const gdn_plan_launch *plan, void *state
   st = make_fold_args(state_addrs, state_block_strides, corr_addrs, corr_block_strides, key_addrs, key_block_strides,
                       decay_addrs, decay_block_strides, layer_groups, config, config_len, ext, &a, &grid, &lds);
   if (st != GDN_OK) return st;
+  if (a.row_list) {
+    set_error("plan_fold: a row list applies to gdn_recoverssm_fold only");
+    return GDN_ERR_INVALID;
+  }
   if (a.rows != p.rows || a.cap != p.cap || a.null_block != p.null_block || a.Q != p.Q) {
     set_error("plan_fold: fold rows/capacity/null block/window (%lld/%lld/%lld/%lld) differ from the plan's "
               "(%lld/%lld/%lld/%lld)",

@@ -74,6 +74,8 @@ class FoldExt(ctypes.Structure):
         ("reserved", c_i32),
         ("source_stride", c_i64),
         ("state_k_stride", c_i64),
+        ("row_list", ctypes.c_void_p),
+        ("row_list_len", c_i64),
     ]
 
 

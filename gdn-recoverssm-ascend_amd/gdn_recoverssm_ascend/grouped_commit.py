@@ -26,7 +26,8 @@ from . import _native as N
 from ._rules import enforce, fail, require
 from ._tables import LayerPages
 from .kernels import (_FOLD_LENGTHS_ARG, NULL_BLOCK_ID, PendingCommit, _conv_spec, _fill_plan_group,
-                      _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _unapplied_lengths, _request_row_map)
+                      _fold_rows_spec, _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _picked_rows,
+                      _request_row_map, _unapplied_lengths)
 
 logger = logging.getLogger("gdn_recoverssm_ascend.grouped_commit")
 
@@ -341,21 +342,18 @@ class DeferredGroupedCommit:
     def flush(self, rows=None) -> None:
         """Fold the given pending rows (every planned row when None) of every
         group now, with the ordinary fold."""
-        pick = None
+        picked = None
         if rows is not None:
-            pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
-            require(bool(((pick >= 0) & (pick < self.num_rows)).all()), "flushed rows must be rows of the pending plan")
-            if pick.numel() == 0:
+            picked = _picked_rows(rows, self.num_rows, self.rows.device)
+            if picked is None:
                 return
-        for bucket, fold, members in self._buckets():
-            if pick is None:
-                lengths = bucket.length
+        for bucket, fold, _ in self._buckets():
+            if picked is None:
+                self._fold(bucket, fold, bucket.length)
             else:
-                lengths = torch.zeros_like(bucket.length)
-                for _, g in members:
-                    idx = (pick + g * bucket.capacity).to(lengths.device)
-                    lengths[idx] = bucket.length[idx]
-            self._fold(bucket, fold, lengths)
+                # Every group of a bucket is a member of the step: the row list
+                # folds the picked rows of each (plan row g * capacity + r).
+                _fold_rows_spec(fold, picked).launch()
 
     def settle(self, next_metadata) -> None:
         """Fold now every pending row that the next step's deferred verifies

@@ -695,7 +695,32 @@ def _make_fold_spec(*, pages: LayerPages, record_rows, key_heads, key_dtype, row
     spec = _LaunchSpec("fold", _lib().gdn_recoverssm_fold, args, ref.device,
                        keepalive=(pages, layer_groups, source, *plan, cfg, ext))
     spec.config = tuple(int(x) for x in config)
+    spec.ext = ext
     return spec
+
+
+def _fold_rows_spec(spec: _LaunchSpec, rows: torch.Tensor) -> _LaunchSpec:
+    """The same fold over the listed plan rows only: ``rows`` is a strictly
+    increasing int32 tensor on the fold's device (the extension block's row
+    list), so the launch has a workgroup per (layer, listed row, head)
+    instead of one per row of the plan."""
+    ext = N.FoldExt.from_buffer_copy(spec.ext)
+    ext.row_list = rows.data_ptr()
+    ext.row_list_len = rows.numel()
+    out = _LaunchSpec(spec.name, spec.fn, spec.args[:-1] + (ctypes.byref(ext),), spec.device,
+                      keepalive=spec.keepalive + (rows, ext))
+    out.config, out.ext = spec.config, ext
+    return out
+
+
+def _picked_rows(rows, num_rows: int, device) -> torch.Tensor | None:
+    """Pending rows named by a flush, checked against the plan's rows, as a
+    sorted int32 tensor of distinct rows on ``device`` (None when empty)."""
+    pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
+    require(bool(((pick >= 0) & (pick < num_rows)).all()), "flushed rows must be rows of the pending plan")
+    if pick.numel() == 0:
+        return None
+    return torch.unique(pick).to(torch.int32).to(device)
 
 
 # Positions in the fold's argument tuple: 4 reference tensors, 8 tables,
@@ -1091,18 +1116,11 @@ class GDNRecoverSSMCommitContext:
         spec = getattr(self, "_deferred_fold", None)
         require(spec is not None, "no deferred commit to flush")
         if rows is not None:
-            pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
-            require(bool(((pick >= 0) & (pick < self._deferred_rows)).all()),
-                    "flushed rows must be rows of the pending plan")
-            if pick.numel() == 0:
+            # The same fold over the picked rows only (a launch sized to them).
+            picked = _picked_rows(rows, self._deferred_rows, self.commit_lens.device)
+            if picked is None:
                 return
-            # The same fold over a length array that keeps only the picked rows.
-            lengths = torch.zeros_like(self.commit_lens)
-            idx = pick.to(lengths.device)
-            lengths[idx] = self.commit_lens[idx]
-            args = list(spec.args)
-            args[_FOLD_LENGTHS_ARG] = lengths.data_ptr()
-            spec = _LaunchSpec(spec.name, spec.fn, tuple(args), spec.device, keepalive=spec.keepalive + (lengths,))
+            spec = _fold_rows_spec(spec, picked)
         if _collect is not None:
             _collect.append(spec)
         else:

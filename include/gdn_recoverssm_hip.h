@@ -92,6 +92,16 @@ typedef struct gdn_fold_ext {
                             table-column stride when the single-context commit
                             reads state_indices directly, kernels.py:1229) */
   int64_t state_k_stride;/* must be 1 */
+  /* No counterpart in the reference: gdn_recoverssm_fold only (NULL for every
+   * other entry point). When row_list is not NULL, the launch folds only the
+   * plan rows it lists: a device int32 array of row_list_len entries
+   * (1 <= row_list_len <= rows), strictly increasing; an entry outside
+   * [0, rows) or not greater than the entry before it folds nothing, so no row
+   * is ever folded twice. The grid then covers layers x row_list_len x heads
+   * instead of every row, which is what a flush of a few rows (requests that
+   * left a deferred batch) costs. */
+  const int32_t *row_list;
+  int64_t row_list_len;
 } gdn_fold_ext;
 
 int gdn_recoverssm_abi_version(void);

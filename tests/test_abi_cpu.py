@@ -180,6 +180,41 @@ def test_plan_outputs_must_not_overlap_its_inputs():
     assert st == N.GDN_ERR_INVALID and b"overlaps the query offsets" in lib.gdn_recoverssm_last_error()
 
 
+def test_fold_row_list_is_checked_before_launch():
+    """A fold row list (gdn_fold_ext.row_list) needs 1..rows entries, and only
+    gdn_recoverssm_fold takes one: the fused plan + fold and the no-allocation
+    commit refuse it. Every call here is rejected before a launch (the device
+    addresses are never dereferenced)."""
+    lib = N.load()
+    fcfg = N.i64_array([4, 1, 4, 2, 4, 16, 4, 8, 0, 128 * 128, 128, 512, 128, 256, 128, 4, 1])
+    tables = [8] * 8
+    plan = [0x10000, 0x20000, 0x30000, 0x40000, 0x50000]  # source and the four plan arrays
+    for n in (0, -1, 5):
+        fext = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1, source_dtype=3, source_stride=1,
+                         row_list=0x60000, row_list_len=n)
+        st = lib.gdn_recoverssm_fold(None, None, None, None, *tables, None, *plan, fcfg, 17, ctypes.byref(fext), None)
+        assert st == N.GDN_ERR_INVALID and b"row list" in lib.gdn_recoverssm_last_error(), n
+    fext = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1, row_list=0x60000, row_list_len=2)
+    groups = N.PlanGroups()
+    g0 = groups[0]
+    g0.state_indices, g0.query_start_loc = 0x60000, 0x70000
+    g0.si_dtype = g0.qsl_dtype = 3
+    g0.si_stride = g0.qsl_stride = 1
+    launch = N.PlanLaunch(sampled=0x50000, sampled_len=4, sampled_stride=1, sampled_dtype=3, num_groups=1,
+                          groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), lens_plan=0x10000,
+                          final_plan=0x20000, boundary_plan=0x30000, boundary_lens_plan=0x40000, num_rows=4,
+                          plan_capacity=8, spec_query_len=4)
+    st = lib.gdn_recoverssm_plan_fold(ctypes.byref(launch), None, None, None, None, *tables, None, fcfg, 17,
+                                      ctypes.byref(fext), None)
+    assert st == N.GDN_ERR_INVALID and b"gdn_recoverssm_fold only" in lib.gdn_recoverssm_last_error()
+    launch = N.PlanLaunch(sampled=8, sampled_len=4, sampled_dtype=3, num_groups=1,
+                          groups=ctypes.cast(groups, ctypes.POINTER(N.PlanGroup)), num_rows=4, spec_query_len=4,
+                          plan_capacity=8)
+    st = lib.gdn_recoverssm_commit_noalloc(ctypes.byref(launch), None, None, None, None, *tables, None, fcfg, 17,
+                                           ctypes.byref(fext), None, None)
+    assert st == N.GDN_ERR_INVALID and b"gdn_recoverssm_fold only" in lib.gdn_recoverssm_last_error()
+
+
 def test_commit_noalloc_rejects_before_touching_the_device():
     """The no-allocation commit refuses caller plan arrays and a plan larger
     than the library's buffer before any HIP call (none is possible here)."""
@@ -250,7 +285,8 @@ int main(void) {
   F(gdn_pending_commit, num_rows)
   F(gdn_gating_ext, softplus_beta) F(gdn_gating_ext, softplus_threshold)
   F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
-  F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride)
+  F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride) F(gdn_fold_ext, row_list)
+  F(gdn_fold_ext, row_list_len)
   F(gdn_plan_group, block_table) F(gdn_plan_group, table_rows) F(gdn_plan_group, num_computed)
   F(gdn_plan_group, computed_dtype) F(gdn_plan_group, num_blocks) F(gdn_plan_group, block_size)
   return 0;

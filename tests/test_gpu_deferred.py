@@ -30,6 +30,7 @@ from gdn_recoverssm_ascend import workloads as W
 from gdn_recoverssm_ascend.kernels import (
     GDNRecoverSSMCommitContext,
     ReplayRecordBuffers,
+    _fold_rows_spec,
     continue_pending,
     gdn_recoverssm_verify,
     gdn_recoverssm_verify_deferred,
@@ -441,6 +442,39 @@ def test_batch_change_with_flush(dev):
         i = inputs1[layer]
         r1 = O.oracle_verify(i.q, i.k, i.v, i.g, i.beta, want[layer], qsl1, idx1, Q)
         _check_verify(outs[layer], recs[1][layer], r1, f"step 1 layer {layer}")
+
+
+def test_flush_of_listed_rows_folds_each_once(dev):
+    """``flush_deferred(rows=...)`` launches the fold over the listed rows
+    only (the fold's row list): rows given in any order and more than once
+    are folded once each, and a device row list that is not strictly
+    increasing folds a repeated row once (the kernel skips an entry not
+    above the one before it). Pages equal the oracle's fold of exactly those
+    rows; every other page, the other rows' final pages included, is
+    unchanged."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=43)
+    s = w.spec
+    L, B, Q = s.layers, s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[1::3] = 1
+    st = _first_step(w, dev, acc)
+    plan, ctx, ckpts = st["plan"], st["ctx"], st["ckpts"]
+    n = plan["commit_lens"]
+    active = [r for r in range(B) if int(n[r]) > 0]
+    assert len(active) >= 5
+    a, b, c = active[0], active[2], active[4]
+    print(f"listed flush: rows {a}, {b}, {c}", flush=True)
+    ctx.flush_deferred(rows=[c, a, c])
+    _fold_rows_spec(ctx._deferred_fold, torch.tensor([b, b], dtype=torch.int32, device=dev)).launch()
+    torch.cuda.synchronize()
+    lengths = torch.zeros_like(n)
+    lengths[[a, b, c]] = n[[a, b, c]]
+    before = [x.cpu() for x in w.checkpoints]
+    want = _oracle_fold(before, st["results"], plan, B, w.num_pages, lengths=lengths)
+    touched = _touched(dict(plan, commit_lens=lengths), B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the listed flush")
 
 
 def test_settle_folds_what_the_verify_does_not_apply(dev):
