@@ -65,8 +65,7 @@ __device__ __forceinline__ uint4 load_stream(__amdgpu_buffer_rsrc_t r, int voff,
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ void store_stream(__amdgpu_buffer_rsrc_t r, int voff, int soff, const uint4 &x) {
-  const fold_u32x4 v = {x.x, x.y, x.z, x.w};
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, kFoldNT);
+  store_b128_settled<kFoldNT>(gdn_u32x4{x.x, x.y, x.z, x.w}, r, voff, soff);
 }
 
 // EARLY: the accepted tokens' corrections and keys are loaded before the state

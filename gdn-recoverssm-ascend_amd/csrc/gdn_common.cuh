@@ -192,6 +192,26 @@ __device__ __forceinline__ uint4 pack16<f16>(const float *in) {
 }
 
 // ----------------------------------------------------------------------------
+// 128-bit buffer store followed by wait states that keep its data registers
+// untouched while the store reads them. With a register soffset the
+// compiler's hazard model lets the next VALU instruction follow such a store
+// at once, and on MI355X that has put a wrong first data dword into memory
+// for some lanes (the value that next instruction read: the FP32 element the
+// f16 conversion after the store was reading). The asm names the data
+// registers, so no instruction that rewrites them moves above the wait, and
+// its memory clobber keeps it behind the store.
+// ----------------------------------------------------------------------------
+#ifndef GDN_STORE_DATA_WAIT
+#define GDN_STORE_DATA_WAIT 4
+#endif
+typedef unsigned gdn_u32x4 __attribute__((ext_vector_type(4)));
+template <int AUX>
+__device__ __forceinline__ void store_b128_settled(gdn_u32x4 v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, AUX);
+  asm volatile("s_nop %1" ::"v"(v), "n"(GDN_STORE_DATA_WAIT) : "memory");
+}
+
+// ----------------------------------------------------------------------------
 // Cross-lane sums inside aligned groups of 8 lanes with DPP (no LDS traffic):
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], then row_half_mirror, which pairs
 // lane i with lane 7-i of the same 8-lane half-row.

@@ -680,22 +680,22 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
             for (int j = g * JR; j < (g + 1) * JR; ++j)
               *reinterpret_cast<uint4 *>(verify_stage[op_slot(j)]) = pack16<S>(h[j]);
             wave_lds_sync();
+            // The round's row runs are read back first, then stored: each
+            // store's wait then holds back only the stores behind it.
+            uint4 x[JR];
 #pragma unroll
-            for (int j = g * JR; j < (g + 1) * JR; ++j) {
-              const uint4 x = *reinterpret_cast<const uint4 *>(verify_stage[row_slot(j)]);
-              __builtin_amdgcn_raw_buffer_store_b128(
-                  __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, x), r, c_voff(j), c_soff(rb, j),
-                  kPolicyNT);
-            }
+            for (int j = 0; j < JR; ++j) x[j] = *reinterpret_cast<const uint4 *>(verify_stage[row_slot(g * JR + j)]);
+#pragma unroll
+            for (int j = 0; j < JR; ++j)
+              store_b128_settled<kPolicyNT>(__builtin_bit_cast(gdn_u32x4, x[j]), r, c_voff(g * JR + j),
+                                            c_soff(rb, g * JR + j));
             wave_lds_sync();
           }
         } else {
 #pragma unroll
           for (int j = 0; j < J; ++j) {
             const int vo = (4 * j + ls) * E < K ? lane_off + j * 64 : kOutOfRange;
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, pack16<S>(h[j])), r, vo,
-                rb * 16 * row_bytes, 0);
+            store_b128_settled<0>(__builtin_bit_cast(gdn_u32x4, pack16<S>(h[j])), r, vo, rb * 16 * row_bytes);
           }
         }
       };

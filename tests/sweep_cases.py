@@ -8,12 +8,15 @@ check it against the oracle.
 
 from __future__ import annotations
 
+import os
 import random
 
 import torch
 
-VERIFY_CASES = 24
-COMMIT_CASES = 16
+# GDN_SWEEP_SCALE=k draws k times as many cases (the default suite keeps 1).
+_SCALE = max(1, int(os.environ.get("GDN_SWEEP_SCALE", "1")))
+VERIFY_CASES = 24 * _SCALE
+COMMIT_CASES = 16 * _SCALE
 
 
 def verify_case(i: int) -> dict:
