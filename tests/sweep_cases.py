@@ -17,6 +17,7 @@ import torch
 _SCALE = max(1, int(os.environ.get("GDN_SWEEP_SCALE", "1")))
 VERIFY_CASES = 24 * _SCALE
 COMMIT_CASES = 16 * _SCALE
+DEFERRED_CASES = 6 * _SCALE
 
 
 def verify_case(i: int) -> dict:
@@ -66,3 +67,22 @@ def commit_case(i: int) -> dict:
     return dict(B=B, H=H, HV=HV, K=K, V=V, Q=Q, L=rng.randint(1, 3), align=rng.random() < 0.5, seed=500 + i,
                 Bk=rng.choice([Q, 8, 16]) if Q <= 8 else 16, key_dtype=key_dtype, state_dtype=state_dtype,
                 packed=packed, qlens=[rng.randint(0, Q) for _ in range(B)], padded=rng.randint(0, 1))
+
+
+def deferred_case(i: int) -> dict:
+    """A carried decode-loop workload for the deferred flow: head dims, GQA
+    ratio, window, dtypes, rows, layers, steps and block size drawn together."""
+    rng = random.Random(9001 + i)
+    state = rng.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16])
+    chunk = 4 if state == torch.float32 else 8
+    K = rng.choice([k for k in (16, 32, 40, 64, 96, 128, 136, 192, 256) if k % chunk == 0])
+    V = rng.choice([8, 16, 40, 64, 100, 128, 192, 256])
+    H = rng.choice([1, 2, 3])
+    HV = H * rng.choice([1, 2, 4])
+    Q = rng.randint(1, 8)
+    return dict(K=K, V=V, Q=Q, H=H, HV=HV,
+                act=rng.choice([torch.bfloat16, torch.float16, torch.float32]), state=state,
+                rows=rng.randint(2, 12), layers=rng.randint(1, 3), steps=rng.randint(2, 4),
+                block_size=rng.choice([b for b in (4, 8, 16) if b >= Q]),  # a block covers one window
+                seed=rng.randint(0, 10_000),
+                empty_row=rng.random() < 0.3)

@@ -26,6 +26,7 @@ import pytest
 import torch
 
 import gdn_oracle as O
+import sweep_cases as SC
 from gdn_recoverssm_ascend import workloads as W
 from gdn_recoverssm_ascend.kernels import (
     GDNRecoverSSMCommitContext,
@@ -337,6 +338,33 @@ def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act, s
     _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
     with state_cache_retain(0):  # the first step's ordinary verify: every row non-temporal
         _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
+
+
+@pytest.mark.parametrize("case", range(SC.DEFERRED_CASES))
+def test_random_deferred_flows(dev, case):
+    """Seeded draws of the deferred flow's options together (head dims, GQA
+    ratio, window, activation and state dtypes, rows, layers, steps, block
+    size, a step in which one row has no token): the deferred flow equals the
+    ordinary flow bit for bit, step by step, and after the final flush."""
+    c = SC.deferred_case(case)
+    print(f"deferred sweep case {case}: {c}", flush=True)
+    w = W.make_workload("decode_loop_l48", layers=c["layers"], rows=c["rows"], key_heads=c["H"],
+                        value_heads=c["HV"], key_dim=c["K"], value_dim=c["V"], window=c["Q"], act_dtype=c["act"],
+                        state_dtype=c["state"], steps=c["steps"], max_position=256, block_size=c["block_size"],
+                        padded_rows=1, seed=c["seed"])
+    s = w.spec
+    gen = torch.Generator().manual_seed(c["seed"] + 1)
+    acc_steps = [W.sample_accepted(s, s.rows, gen) for _ in range(c["steps"])]
+    acc_steps[0] = acc_steps[0].clamp(min=1)  # a small batch could otherwise commit nothing at all
+    qsl_steps = [w.meta.query_start_loc.clone() for _ in range(c["steps"])]
+    if c["empty_row"]:
+        lens = torch.full((s.rows,), s.window, dtype=torch.int32)
+        lens[case % s.rows] = 0
+        q2 = torch.zeros(s.rows + 1, dtype=torch.int32)
+        q2[1:] = torch.cumsum(lens, 0)
+        qsl_steps[-1] = q2
+    ref = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
+    _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
 
 
 def _first_step(w, dev, acc):
