@@ -18,6 +18,7 @@ _SCALE = max(1, int(os.environ.get("GDN_SWEEP_SCALE", "1")))
 VERIFY_CASES = 24 * _SCALE
 COMMIT_CASES = 16 * _SCALE
 DEFERRED_CASES = 6 * _SCALE
+COORDINATOR_CASES = 6 * _SCALE
 
 
 def verify_case(i: int) -> dict:
@@ -86,3 +87,21 @@ def deferred_case(i: int) -> dict:
                 block_size=rng.choice([b for b in (4, 8, 16) if b >= Q]),  # a block covers one window
                 seed=rng.randint(0, 10_000),
                 empty_row=rng.random() < 0.3)
+
+
+def coordinator_case(i: int) -> dict:
+    """One grouped commit through the coordinator: 1-7 cache groups on the
+    same rows, each with its own layer count and record layout (typed keys in
+    the activation dtype or FP32, or packed records), head dims, window and
+    state dtype shared by the step."""
+    rng = random.Random(11001 + i)
+    state = rng.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16])
+    chunk = 4 if state == torch.float32 else 8
+    K = rng.choice([k for k in (16, 32, 40, 64, 96, 128, 136, 192, 256) if k % chunk == 0])
+    H = rng.choice([1, 2, 3])
+    n = rng.randint(1, 7)
+    return dict(n_groups=n, align=rng.random() < 0.6, B=rng.randint(2, 8), H=H, HV=H * rng.choice([1, 2, 4]), K=K,
+                V=rng.choice([8, 16, 40, 64, 100, 128]), Q=rng.randint(1, 8), state=state,
+                layers=[rng.randint(1, 3) for _ in range(n)],
+                layouts=[rng.choice(["bf16", "bf16", "f32", "packed"]) for _ in range(n)],
+                seed=rng.randint(0, 10_000))

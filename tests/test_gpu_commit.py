@@ -547,6 +547,74 @@ def test_coordinator_groups_against_oracle(dev, n_groups, align, B, seed, hetero
     assert all(coord._buckets[k] is first[k] for k in first)
 
 
+@pytest.mark.parametrize("case", range(SC.COORDINATOR_CASES))
+def test_random_coordinator_commits(dev, case):
+    """Seeded draws of a grouped commit through the coordinator: 1-7 cache
+    groups on one set of shuffled request rows, each with its own layer count
+    and record layout (groups of different layouts commit in separate
+    buckets), none or align mode, head dims, window and state dtype: plans,
+    folded pages, conv states and the align publication across every bucket
+    against the oracle, group by group."""
+    c = SC.coordinator_case(case)
+    print(f"coordinator sweep case {case}: {c}", flush=True)
+    B, Q, align, n_groups = c["B"], c["Q"], c["align"], c["n_groups"]
+    gen = torch.Generator().manual_seed(c["seed"])
+    request_rows = torch.randperm(B, generator=gen).tolist()
+    sampled = torch.randint(0, Q + 1, (B,), generator=gen, dtype=torch.int32)
+    sampled[0] = max(int(sampled[0]), 1)
+    groups = []
+    for g in range(n_groups):
+        layout = c["layouts"][g]
+        groups.append(_group(B, c["H"], c["HV"], c["K"], c["V"], Q, c["layers"][g], align=align,
+                             seed=c["seed"] + 7 * g, page_offset=3 * g, state_dtype=c["state"],
+                             key_dtype=torch.float32 if layout == "f32" else torch.bfloat16,
+                             packed=layout == "packed"))
+    for G in groups[1:]:
+        G["qsl"] = groups[0]["qsl"].clone()
+        if align:
+            G["C"] = groups[0]["C"].clone()
+    metas, devs = [], []
+    for G in groups:
+        if align:
+            src_col = torch.clamp(G["C"].long() - 1, min=0) // G["Bk"]
+            table = torch.zeros_like(G["table"])
+            for r in range(B):
+                for j in range(3):
+                    table[r, int(src_col[r]) + j] = 1 + 3 * r + j
+            G["table"], G["src"] = table, table[torch.arange(B), src_col].clone()
+        _index_by_request(G, request_rows)
+        ckpts, convs, recs = _to_dev(G, dev)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=Q, max_num_reqs=B)
+        devs.append((ckpts, convs))
+        metas.append(_entry(G, ctx, dev, request_rows).metadata)
+    mapping = torch.randperm(B + 2, generator=gen)[:B].to(torch.int32)
+    cols = torch.full((B + 2,), -9, dtype=torch.int32)
+    accp = torch.full((B + 2,), 7, dtype=torch.int32)
+    cols_d, accp_d = cols.to(dev), accp.to(dev)
+    coord = GroupedCommitCoordinator()
+    coord.commit(metas, sampled.to(dev), mapping.to(dev), cols_d, accp_d)
+    torch.cuda.synchronize()
+    assert coord.last_group_count == n_groups
+    want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, align, B)
+    if align:
+        assert cols_d.cpu().tolist() == want["persistent_cols"].tolist(), "publication differs"
+        assert accp_d.cpu().tolist() == want["persistent_accepted"].tolist(), "publication differs"
+    for gi, G in enumerate(groups):
+        seg = slice(gi * B, gi * B + B)
+        corrs, keys, decays = _planes(G)
+        wstate = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=want["source"][seg], lengths=want["length"][seg],
+                               final=want["final"][seg], boundary=want["boundary"][seg],
+                               boundary_len=want["boundary_len"][seg], rows=B, num_blocks=G["NB"], record_rows=B)
+        targeted = set(want["final"][seg].tolist()) | set(want["boundary"][seg].tolist())
+        _check_states(devs[gi][0], wstate, c["state"], targeted)
+        wconv = O.oracle_conv_compact(G["convs"], source=want["source"][seg], lengths=want["length"][seg],
+                                      final=want["final"][seg], boundary=want["boundary"][seg],
+                                      boundary_len=want["boundary_len"][seg], history=HIST, num_blocks=G["NB"],
+                                      rows=B, align=align)
+        for li, (got, w) in enumerate(zip(devs[gi][1], wconv)):
+            assert torch.equal(got.cpu(), w), f"group {gi} layer {li}: conv states differ"
+
+
 @pytest.mark.parametrize("align", [False, True])
 def test_commit_int64_metadata(dev, align):
     """int64 accepted counts, state indices (a column view of a wider table),
