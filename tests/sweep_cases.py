@@ -19,6 +19,7 @@ VERIFY_CASES = 24 * _SCALE
 COMMIT_CASES = 16 * _SCALE
 DEFERRED_CASES = 6 * _SCALE
 COORDINATOR_CASES = 6 * _SCALE
+GATED_CASES = 6 * _SCALE
 
 
 def verify_case(i: int) -> dict:
@@ -105,3 +106,26 @@ def coordinator_case(i: int) -> dict:
                 layers=[rng.randint(1, 3) for _ in range(n)],
                 layouts=[rng.choice(["bf16", "bf16", "f32", "packed"]) for _ in range(n)],
                 seed=rng.randint(0, 10_000))
+
+
+def gated_case(i: int) -> dict:
+    """The gated verify (gating and q/k L2 norm fused in): head dims, GQA
+    ratio, window, ragged / null / out-of-range rows, activation and state
+    dtypes, raw a / b in the activation dtype or FP32, A_log / dt_bias in any
+    float dtype."""
+    rng = random.Random(13001 + i)
+    state = rng.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16])
+    chunk = 4 if state == torch.float32 else 8
+    K = rng.choice([k for k in (16, 32, 40, 64, 96, 128, 136, 192, 256) if k % chunk == 0])
+    H = rng.choice([1, 2, 3])
+    Q = rng.randint(1, 8)
+    B = rng.randint(1, 7)
+    qlens = [rng.randint(0, Q) for _ in range(B)]
+    qlens[0] = max(qlens[0], 1)
+    rows = list(range(B))
+    rng.shuffle(rows)
+    act = rng.choice([torch.bfloat16, torch.float16, torch.float32])
+    return dict(B=B, H=H, HV=H * rng.choice([1, 2, 4]), K=K, V=rng.choice([8, 16, 48, 64, 100, 128, 192, 256]), Q=Q,
+                qlens=qlens, null_rows=tuple(rows[: rng.randint(0, 1)]), oob_rows=tuple(rows[1: 1 + rng.randint(0, 1)]),
+                act=act, state=state, ab=rng.choice([act, torch.float32]),
+                param=rng.choice([torch.float32, torch.bfloat16, torch.float16]), seed=rng.randint(0, 10_000))
