@@ -7,6 +7,7 @@ records and pages (they launch the same kernels through the C ABI)."""
 import pytest
 import torch
 
+import sweep_cases as SC
 from gdn_recoverssm_ascend import torch_ops  # noqa: F401  (registers the operators)
 from gdn_recoverssm_ascend import workloads as W
 from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext, ReplayRecordBuffers, gdn_recoverssm_verify
@@ -20,13 +21,14 @@ def dev(gpu_device):
     return gpu_device
 
 
-def _workload(dev):
-    w = W.make_workload("align_b256", rows=12, key_heads=2, value_heads=4, padded_rows=1, seed=3)
-    return w.to(dev)
+def _workload(dev, **kw):
+    spec = dict(rows=12, key_heads=2, value_heads=4, padded_rows=1, seed=3)
+    spec.update(kw)
+    return W.make_workload("align_b256", **spec).to(dev)
 
 
-def test_verify_operator_equals_api(dev):
-    w = _workload(dev)
+def test_verify_operator_equals_api(dev, **kw):
+    w = _workload(dev, **kw)
     s, m, inp = w.spec, w.meta, w.inputs[0]
     B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
     runs = []
@@ -50,8 +52,8 @@ def test_verify_operator_equals_api(dev):
     assert bool((runs[0][0] != -7.0).any())
 
 
-def test_fold_operator_equals_api(dev):
-    w = _workload(dev)
+def test_fold_operator_equals_api(dev, _any_commit=True, **kw):
+    w = _workload(dev, **kw)
     s, m = w.spec, w.meta
     B, Q, H, HV, K, V = s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
     gen = torch.Generator(device=dev).manual_seed(5)
@@ -80,4 +82,23 @@ def test_fold_operator_equals_api(dev):
     fold.launch()
     torch.cuda.synchronize()
     assert torch.equal(via_op, w.checkpoints[0])
-    assert not torch.equal(via_op, pages0)  # the step committed something
+    if _any_commit:
+        assert not torch.equal(via_op, pages0)  # the step committed something
+
+
+def _random_shape(case):
+    c = SC.deferred_case(case)
+    print(f"operator sweep case {case}: {c}", flush=True)
+    return dict(rows=c["rows"], key_heads=c["H"], value_heads=c["HV"], key_dim=c["K"], value_dim=c["V"],
+                window=c["Q"], act_dtype=c["act"], state_dtype=c["state"], block_size=max(c["block_size"], c["Q"]),
+                seed=c["seed"])
+
+
+@pytest.mark.parametrize("case", range(SC.DEFERRED_CASES))
+def test_random_operators_equal_api(dev, case):
+    """Both operators over seeded random shapes (head dims, GQA ratio, window,
+    activation and state dtypes, rows, block size): bit-identical to the API's
+    own launches."""
+    shape = _random_shape(case)
+    test_verify_operator_equals_api(dev, **shape)
+    test_fold_operator_equals_api(dev, _any_commit=False, **shape)  # a small batch may accept nothing

@@ -19,6 +19,7 @@ import pytest
 import torch
 
 import gdn_oracle as O
+import sweep_cases as SC
 from gdn_recoverssm_ascend import _native as N
 from gdn_recoverssm_ascend.grouped_commit import GroupedCommitBucket
 from gdn_recoverssm_ascend.kernels import GDNRecoverSSMCommitContext
@@ -190,3 +191,33 @@ def test_grouped_bucket_two_calls(dev, align):
         assert torch.equal(ref[1], got[1]) and torch.equal(ref[2], got[2]), f"{what}: publication differs"
         if align:
             assert int((got[2] == 1).sum()) > 0, f"{what}: nothing was published"
+
+
+@pytest.mark.parametrize("case", range(SC.COMMIT_CASES // 2))
+def test_random_configurations_two_calls(dev, case):
+    """Two seeded random commit draws in a row (head dims, GQA ratio, window,
+    layers, none / align mode and block size, state and key dtypes, packed
+    records, short and empty windows, a padded row): each call of the
+    no-allocation commit bit-identical to the commit with caller-owned plan
+    arrays, the second reading none of what the first left in the buffer."""
+    for call, draw in enumerate((2 * case, 2 * case + 1)):
+        c = SC.commit_case(draw)
+        print(f"no-allocation sweep case {case} call {call}: {c}", flush=True)
+        B, Q, align = c["B"], c["Q"], c["align"]
+        G = _group(B, c["H"], c["HV"], c["K"], c["V"], Q, c["L"], align=align, seed=c["seed"], Bk=c["Bk"],
+                   key_dtype=c["key_dtype"], state_dtype=c["state_dtype"], packed=c["packed"], qlens=c["qlens"])
+        if c["padded"]:
+            G["src"][B // 2] = -1
+        (rc, rv, rr), (gc, gv, gr) = _copies(G, dev)
+        meta = dict(block_table=G["table"].to(dev) if align else None,
+                    num_computed_tokens=G["C"].to(dev) if align else None, mamba_block_size=G["Bk"])
+        acc, src, qsl = G["acc"].to(dev), G["src"].to(dev), G["qsl"].to(dev)
+        ref_ctx = GDNRecoverSSMCommitContext.from_tensors(rv, rc, rr, spec_query_len=Q, max_num_reqs=B + 3)
+        ref_ctx.commit(acc, src, qsl, **meta)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(gv, gc, gr, spec_query_len=Q, max_num_reqs=B + 3)
+        _commit_noalloc(ctx.make_commit_specs(acc, src, qsl, **meta), dev)
+        torch.cuda.synchronize()
+        for li, (a, b) in enumerate(zip(rc, gc)):
+            assert torch.equal(a, b), f"draw {draw}: layer {li} pages differ"
+        for li, (a, b) in enumerate(zip(rv, gv)):
+            assert torch.equal(a, b), f"draw {draw}: layer {li} conv states differ"
