@@ -164,6 +164,75 @@ __global__ __launch_bounds__(64) void publish_kernel(const int64_t *__restrict__
   }
 }
 
+// What a settle of a deferred commit folds (one workgroup). Pending row r <
+// num_rows of group g is applied by the next verify when a next row b of that
+// group has rows[b] == r and b's next state index is r's final page (the
+// test by which the deferred verify applies a pending commit); the applied
+// rows are marked in an LDS bitmap first, so every output entry is then
+// written once: 0 for an applied row, the plan's length otherwise. The rows
+// left with a length in some group are listed in ascending order (a prefix
+// sum over each tile of 1024 rows), and their number stored last.
+constexpr int kSettleThreads = 1024;
+constexpr int kSettleWaves = kSettleThreads / 64;
+
+struct SettleNext {
+  const void *si[GDN_SETTLE_MAX_GROUPS];
+  int64_t stride[GDN_SETTLE_MAX_GROUPS];
+  int64_t rows[GDN_SETTLE_MAX_GROUPS];
+  int32_t dtype[GDN_SETTLE_MAX_GROUPS];
+};
+
+__global__ __launch_bounds__(kSettleThreads) void settle_kernel(const int32_t *__restrict__ lengths,
+                                                                const int32_t *__restrict__ finals, int32_t groups,
+                                                                int64_t cap, int32_t num_rows,
+                                                                const int32_t *__restrict__ rows, SettleNext nx,
+                                                                int32_t *__restrict__ out, int32_t *__restrict__ list,
+                                                                int32_t *__restrict__ count) {
+  constexpr int kWords = GDN_SETTLE_MAX_ROWS / 32;
+  __shared__ uint32_t applied[GDN_SETTLE_MAX_GROUPS][kWords];
+  __shared__ int32_t wave_count[kSettleWaves];
+  const int tid = int(threadIdx.x);
+  const int words = (num_rows + 31) / 32;
+  for (int g = 0; g < groups; ++g)
+    for (int i = tid; i < words; i += kSettleThreads) applied[g][i] = 0u;
+  __syncthreads();
+  for (int g = 0; g < groups; ++g) {
+    for (int64_t b = tid; b < nx.rows[g]; b += kSettleThreads) {
+      const int32_t r = rows[b];
+      if (r >= 0 && r < num_rows && load_index(nx.si[g], b * nx.stride[g], nx.dtype[g]) == int64_t(finals[g * cap + r]))
+        atomicOr(&applied[g][r >> 5], 1u << (r & 31));
+    }
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  int32_t listed = 0;  // rows listed by the tiles before this one (the same in every thread)
+  for (int64_t r0 = 0; r0 < cap; r0 += kSettleThreads) {
+    const int64_t r = r0 + tid;
+    bool left = false;
+    if (r < cap) {
+      for (int g = 0; g < groups; ++g) {
+        const int64_t i = g * cap + r;
+        const bool hit = r < num_rows && ((applied[g][r >> 5] >> (r & 31)) & 1u);
+        const int32_t n = hit ? 0 : lengths[i];
+        out[i] = n;
+        left = left || (r < num_rows && n > 0);
+      }
+    }
+    const uint64_t m = __ballot(left);
+    if (lane == 0) wave_count[wave] = __popcll(m);
+    __syncthreads();
+    int32_t before = listed, tile = 0;
+    for (int k = 0; k < kSettleWaves; ++k) {
+      before += k < wave ? wave_count[k] : 0;
+      tile += wave_count[k];
+    }
+    if (left) list[before + __popcll(m & ((uint64_t(1) << lane) - 1))] = int32_t(r);
+    listed += tile;
+    __syncthreads();  // wave_count is rewritten by the next tile
+  }
+  if (tid == 0) *count = listed;
+}
+
 static bool index_dtype_ok(int32_t dt) { return dt == GDN_DT_I32 || dt == GDN_DT_I64; }
 
 }  // namespace gdn
@@ -472,6 +541,76 @@ extern "C" int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_bu
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     set_error("publish: launch failed: %s", hipGetErrorString(err));
+    return GDN_ERR_LAUNCH;
+  }
+  return GDN_OK;
+}
+
+extern "C" int gdn_recoverssm_settle(const int32_t *lengths, const int32_t *finals, int64_t num_groups,
+                                     int64_t capacity, int64_t num_rows, const int32_t *rows, int64_t rows_len,
+                                     const gdn_settle_next *next, int32_t *out_lengths, int32_t *row_list,
+                                     int32_t *row_count, void *stream) {
+  if (num_groups < 1 || num_groups > GDN_SETTLE_MAX_GROUPS || capacity < 1 || num_rows < 0 || num_rows > capacity ||
+      num_rows > GDN_SETTLE_MAX_ROWS || num_groups * capacity > 0x7fffffffLL) {
+    set_error("settle: %lld groups of %lld plan rows with %lld pending rows (1..%d groups, pending rows <= plan "
+              "rows and <= %d)",
+              (long long)num_groups, (long long)capacity, (long long)num_rows, GDN_SETTLE_MAX_GROUPS,
+              GDN_SETTLE_MAX_ROWS);
+    return GDN_ERR_INVALID;
+  }
+  if (!lengths || !finals || !next || !out_lengths || !row_list || !row_count) {
+    set_error("settle: missing plan lengths, final pages, next batch, output lengths, row list or count");
+    return GDN_ERR_INVALID;
+  }
+  SettleNext nx{};
+  int64_t most = 0;
+  for (int64_t g = 0; g < num_groups; ++g) {
+    const gdn_settle_next &n = next[g];
+    if (n.rows < 0 || (n.rows > 0 && (!n.state_indices || !rows || rows_len < n.rows || !index_dtype_ok(n.dtype) ||
+                                      n.stride < 0))) {
+      set_error("settle: group %lld: the row map (%lld entries) and the next state indices (int32/int64, stride "
+                ">= 0) must cover its %lld next rows",
+                (long long)g, (long long)rows_len, (long long)n.rows);
+      return GDN_ERR_INVALID;
+    }
+    nx.si[g] = n.state_indices;
+    nx.stride[g] = n.stride;
+    nx.rows[g] = n.rows;
+    nx.dtype[g] = n.dtype;
+    most = std::max(most, n.rows);
+  }
+  // The outputs are written while the inputs are read: they share memory
+  // with no input and with each other (the plan's own lengths stay).
+  const int64_t entries = num_groups * capacity;
+  const PlanSpan outs[] = {plan_span("output lengths", out_lengths, entries, 1, 4),
+                           plan_span("row list", row_list, std::max<int64_t>(num_rows, 1), 1, 4),
+                           plan_span("row count", row_count, 1, 1, 4)};
+  std::vector<PlanSpan> ins = {plan_span("plan lengths", lengths, entries, 1, 4),
+                               plan_span("final pages", finals, entries, 1, 4),
+                               plan_span("row map", rows, most, 1, 4)};
+  for (int64_t g = 0; g < num_groups; ++g)
+    ins.push_back(plan_span("next state indices", next[g].state_indices, next[g].rows, next[g].stride,
+                            next[g].dtype == GDN_DT_I64 ? 8 : 4));
+  for (size_t i = 0; i < 3; ++i) {
+    for (const PlanSpan &x : ins) {
+      if (spans_overlap(outs[i], x)) {
+        set_error("settle: the %s overlaps the %s", outs[i].what, x.what);
+        return GDN_ERR_INVALID;
+      }
+    }
+    for (size_t j = i + 1; j < 3; ++j) {
+      if (spans_overlap(outs[i], outs[j])) {
+        set_error("settle: the %s overlaps the %s", outs[i].what, outs[j].what);
+        return GDN_ERR_INVALID;
+      }
+    }
+  }
+  hipLaunchKernelGGL(settle_kernel, dim3(1), dim3(kSettleThreads), 0, static_cast<hipStream_t>(stream), lengths,
+                     finals, int32_t(num_groups), capacity, int32_t(num_rows), rows, nx, out_lengths, row_list,
+                     row_count);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("settle: launch failed: %s", hipGetErrorString(err));
     return GDN_ERR_LAUNCH;
   }
   return GDN_OK;

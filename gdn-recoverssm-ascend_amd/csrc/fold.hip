@@ -340,6 +340,27 @@ __global__ __launch_bounds__(kFoldThreads) void fold_kernel(FoldArgs a) {
   fold_body<S, KT, false, ORDER>(a, nullptr, blockIdx.x);
 }
 
+// The first min(*row_count, grid_rows) entries of the row list, a count the
+// device wrote: a fixed grid whose workgroups take the (layer, listed row,
+// head) tiles in turn, so a list that the host cannot size costs the tiles it
+// names instead of a launch over every row. The count is read through the
+// scalar cache (written by an earlier launch, read-only here), so the loop
+// bound and every barrier in it are uniform.
+template <typename S, typename KT>
+__global__ __launch_bounds__(kFoldThreads) void fold_listed_kernel(FoldArgs a, const int32_t *row_count,
+                                                                   int64_t layers) {
+  warm_kernel_args<int(sizeof(FoldArgs) + sizeof(void *) + sizeof(int64_t))>();
+  const auto *count =
+      reinterpret_cast<const __attribute__((address_space(4))) int32_t *>(reinterpret_cast<uintptr_t>(row_count));
+  const int64_t listed = *count;
+  a.grid_rows = listed < 0 ? 0 : listed < a.grid_rows ? listed : a.grid_rows;
+  const int64_t tiles = layers * a.grid_rows * a.heads;
+  for (int64_t w = blockIdx.x; w < tiles; w += gridDim.x) {
+    __syncthreads();  // the previous tile's records in LDS are no longer read
+    fold_body<S, KT, false, kOrderDefault>(a, nullptr, w);
+  }
+}
+
 // The first `writers` workgroups store the plan (one thread per row); the rest
 // fold, each planning its own row.
 template <typename S, typename KT, int ORDER>
@@ -368,6 +389,22 @@ static void launch_fold_key(int key_dtype, dim3 grid, size_t lds, hipStream_t s,
     default: GDN_FOLD_LAUNCH(float) break;
   }
 #undef GDN_FOLD_LAUNCH
+}
+
+template <typename S>
+static void launch_fold_listed(int key_dtype, dim3 grid, size_t lds, hipStream_t s, const FoldArgs &a,
+                               const int32_t *row_count, int64_t layers) {
+  switch (key_dtype) {
+    case GDN_DT_BF16:
+      hipLaunchKernelGGL((fold_listed_kernel<S, bf16>), grid, dim3(kFoldThreads), lds, s, a, row_count, layers);
+      break;
+    case GDN_DT_F16:
+      hipLaunchKernelGGL((fold_listed_kernel<S, f16>), grid, dim3(kFoldThreads), lds, s, a, row_count, layers);
+      break;
+    default:
+      hipLaunchKernelGGL((fold_listed_kernel<S, float>), grid, dim3(kFoldThreads), lds, s, a, row_count, layers);
+      break;
+  }
 }
 
 template <typename S>
@@ -487,6 +524,9 @@ static int make_fold_args(const int64_t *state_addrs, const int64_t *state_block
     }
     a.row_list = ext->row_list;
     a.grid_rows = ext->row_list_len;
+  } else if (ext->row_count) {
+    set_error("fold: a row count applies to a row list");
+    return GDN_ERR_INVALID;
   }
   *out = a;
   *grid = layers * a.grid_rows * heads;
@@ -501,6 +541,22 @@ static int launch_fold(const gdn_fold_ext *ext, int64_t grid, size_t lds, const 
     return GDN_ERR_UNSUPPORTED;
   }
   auto s = static_cast<hipStream_t>(stream);
+  if (a.row_list && ext->row_count) {
+    // The grid loops over the tiles of the listed rows the device counted.
+    const int64_t layers = grid / (a.grid_rows * a.heads);
+    const dim3 g{unsigned(grid < GDN_FOLD_LISTED_GRID ? grid : GDN_FOLD_LISTED_GRID)};
+    switch (ext->state_dtype) {
+      case GDN_DT_BF16: launch_fold_listed<bf16>(ext->key_dtype, g, lds, s, a, ext->row_count, layers); break;
+      case GDN_DT_F16: launch_fold_listed<f16>(ext->key_dtype, g, lds, s, a, ext->row_count, layers); break;
+      default: launch_fold_listed<float>(ext->key_dtype, g, lds, s, a, ext->row_count, layers); break;
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+      set_error("fold: launch failed: %s", hipGetErrorString(err));
+      return GDN_ERR_LAUNCH;
+    }
+    return GDN_OK;
+  }
   const dim3 g{unsigned(grid)};
   // Records first for grids of a few rounds, when they fit the early passes.
   // (make_fold_args has checked that every window's records fit 32-bit offsets.)

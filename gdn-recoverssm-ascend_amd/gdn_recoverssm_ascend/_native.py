@@ -76,7 +76,23 @@ class FoldExt(ctypes.Structure):
         ("state_k_stride", c_i64),
         ("row_list", ctypes.c_void_p),
         ("row_list_len", c_i64),
+        ("row_count", ctypes.c_void_p),
     ]
+
+
+class SettleNext(ctypes.Structure):
+    """gdn_settle_next: one plan group's next batch for gdn_recoverssm_settle."""
+    _fields_ = [
+        ("state_indices", ctypes.c_void_p),
+        ("stride", c_i64),
+        ("rows", c_i64),
+        ("dtype", c_i32),
+        ("reserved", c_i32),
+    ]
+
+
+SETTLE_MAX_GROUPS = 3
+SETTLE_MAX_ROWS = 65536
 
 
 class GatingExt(ctypes.Structure):
@@ -223,6 +239,9 @@ def load() -> ctypes.CDLL:
         ]
         lib.gdn_recoverssm_set_state_cache_retain.restype = c_i64
         lib.gdn_recoverssm_set_state_cache_retain.argtypes = [c_i64]
+        lib.gdn_recoverssm_settle.restype = ctypes.c_int
+        lib.gdn_recoverssm_settle.argtypes = [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,
+                                              ctypes.POINTER(SettleNext), c_vp, c_vp, c_vp, c_vp]
         version = lib.gdn_recoverssm_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"GDN RecoverSSM HIP library ABI mismatch: {version} != {ABI_VERSION}")
@@ -262,6 +281,7 @@ def exported_symbols() -> tuple[str, ...]:
         "gdn_recoverssm_conv_compact",
         "gdn_recoverssm_publish",
         "gdn_recoverssm_set_state_cache_retain",
+        "gdn_recoverssm_settle",
     )
 
 

@@ -27,7 +27,7 @@ from ._rules import enforce, fail, require
 from ._tables import LayerPages
 from .kernels import (_FOLD_LENGTHS_ARG, NULL_BLOCK_ID, PendingCommit, _conv_spec, _fill_plan_group,
                       _fold_rows_spec, _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _picked_rows,
-                      _request_row_map, _unapplied_lengths)
+                      _request_row_map, _settle_spec)
 
 logger = logging.getLogger("gdn_recoverssm_ascend.grouped_commit")
 
@@ -216,8 +216,12 @@ class GroupedCommitBucket:
         self.layer_groups = torch.repeat_interleave(torch.arange(len(contexts), dtype=torch.int32),
                                                     per_context).to(self.device)
         # Plan arrays: group g's row r at g * capacity + r.
-        for name in ("source", "length", "final", "boundary", "boundary_len", "valid", "col"):
+        # settle_length / settle_rows / settle_count: what a deferred settle
+        # folds (lengths, the rows it lists, their number).
+        for name in ("source", "length", "final", "boundary", "boundary_len", "valid", "col", "settle_length"):
             setattr(self, name, torch.zeros(self.capacity * len(contexts), dtype=torch.int32, device=self.device))
+        self.settle_rows = torch.zeros(self.capacity, dtype=torch.int32, device=self.device)
+        self.settle_count = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     checkpoints = property(lambda self: self.pages.checkpoints)
     conv_states = property(lambda self: self.pages.conv_states)
@@ -363,14 +367,19 @@ class DeferredGroupedCommit:
         Decided on the device; call it before the next verifies."""
         nxt = _step_entries(next_metadata)
         require(len(nxt) == len(self._entries), "the next step has another number of committing groups")
+        if self.num_rows == 0:
+            return  # nothing is pending
         for bucket, fold, members in self._buckets():
-            lengths = bucket.length.clone()
+            # The device decides which rows to fold and lists them in the
+            # bucket's own arrays (the plan's lengths stay for the verifies),
+            # one launch for its groups; the fold covers the listed rows only.
+            nexts = [None] * (bucket.length.shape[0] // bucket.capacity)
             for i, g in members:
-                seg = slice(g * bucket.capacity, (g + 1) * bucket.capacity)
-                si = nxt[i].payload.state_indices
-                require(self.rows.shape[0] >= si.shape[0], "the pending row map does not cover the next batch")
-                lengths[seg] = _unapplied_lengths(bucket.length[seg], bucket.final[seg], self.num_rows, self.rows, si)
-            self._fold(bucket, fold, lengths)
+                nexts[g] = nxt[i].payload.state_indices
+            _settle_spec(bucket.length, bucket.final, bucket.capacity, self.num_rows, self.rows, nexts,
+                         bucket.settle_length, bucket.settle_rows, bucket.settle_count).launch()
+            _fold_rows_spec(fold, bucket.settle_rows, bucket.settle_count, lengths=bucket.settle_length,
+                            listed=self.num_rows).launch()
 
 
 # ---------------------------------------------------------------------------

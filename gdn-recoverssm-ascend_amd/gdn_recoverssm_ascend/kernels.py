@@ -526,7 +526,7 @@ def _request_row_map(num_rows: int, previous_requests: Sequence, next_requests: 
         seen.add(req)
         mapping.append(where.get(req, -1))
     left = sorted(r for req, r in where.items() if req not in seen)
-    return torch.tensor(mapping if mapping else [-1], dtype=torch.int32, device=device), left
+    return _to_device_rows(mapping if mapping else [-1], device), left
 
 
 _PENDING_RULES = (
@@ -601,25 +601,51 @@ def gdn_recoverssm_verify_deferred(
     return _run_verify(c, scale, out, _collect, pending=(struct, (pending, rec)))
 
 
-def _unapplied_lengths(lengths: torch.Tensor, finals: torch.Tensor, num_rows: int, rows: torch.Tensor,
-                       next_state_indices: torch.Tensor) -> torch.Tensor:
-    """The plan's lengths with every pending row that a next row applies set
-    to 0 (device ops only). Next row b applies pending row r = rows[b] when
-    0 <= r < num_rows and next_state_indices[b] == finals[r], the deferred
-    verify's own test; its other tests (accepted length 1..Q, pages in range)
-    are the fold's as well, so a row failing them is a no-op either way."""
-    nb = next_state_indices.shape[0]
-    out = lengths.clone()
-    if nb == 0 or num_rows == 0:
-        return out
-    r = rows[:nb].to(torch.int64)
-    ok = (r >= 0) & (r < num_rows)
-    safe = torch.where(ok, r, torch.zeros_like(r))
-    ok = ok & (next_state_indices.to(torch.int64) == finals[safe].to(torch.int64))
-    applied = torch.zeros(num_rows + 1, dtype=torch.int32, device=lengths.device)
-    applied.scatter_(0, torch.where(ok, r, torch.full_like(r, num_rows)), 1)
-    out[:num_rows] = torch.where(applied[:num_rows] > 0, torch.zeros_like(out[:num_rows]), out[:num_rows])
-    return out
+def _settle_spec(lengths: torch.Tensor, finals: torch.Tensor, capacity: int, num_rows: int, rows: torch.Tensor,
+                 nexts: Sequence, out: torch.Tensor, row_list: torch.Tensor, row_count: torch.Tensor) -> _LaunchSpec:
+    """The launch (gdn_recoverssm_settle) that decides on the device what a
+    settle of a deferred commit folds, for the plan groups of one plan:
+    ``lengths`` / ``finals`` hold ``len(nexts)`` groups of ``capacity`` plan
+    rows, ``nexts[g]`` is group g's next state indices (None: a group outside
+    the next step). Group g's pending row r < ``num_rows`` is applied by the
+    next verify when some next row b has rows[b] == r and nexts[g][b] is r's
+    final page (the deferred verify's own test); ``out`` gets the plan's
+    lengths with 0 for the applied rows, ``row_list`` / ``row_count`` the
+    ascending rows left with a length in some group and their number, for a
+    fold over them (``_fold_rows_spec``). Nothing is synchronised with the
+    host."""
+    groups = len(nexts)
+    require(1 <= groups <= N.SETTLE_MAX_GROUPS, f"a settle covers 1..{N.SETTLE_MAX_GROUPS} plan groups")
+    require(0 <= num_rows <= min(capacity, N.SETTLE_MAX_ROWS),
+            f"a settle covers at most {N.SETTLE_MAX_ROWS} pending rows")
+    dev = out.device
+    require(rows.dtype == torch.int32 and rows.is_contiguous() and rows.device == dev,
+            "the pending row map must be a contiguous int32 tensor on the plan's device")
+    table = (N.SettleNext * groups)()
+    held = [lengths, finals, rows, out, row_list, row_count, table]
+    for g, nxt in enumerate(nexts):
+        if nxt is None:
+            continue
+        require(nxt.ndim == 1 and nxt.device == dev and nxt.dtype in (torch.int32, torch.int64),
+                "next state indices must be a 1-D int32 or int64 tensor on the plan's device")
+        require(rows.shape[0] >= nxt.shape[0], "the pending row map does not cover the next batch")
+        table[g].state_indices = nxt.data_ptr()
+        table[g].stride = nxt.stride(0) if nxt.shape[0] > 1 else 1
+        table[g].rows = nxt.shape[0]
+        table[g].dtype = N.dtype_code(nxt.dtype)
+        held.append(nxt)
+    args = (lengths.data_ptr(), finals.data_ptr(), groups, int(capacity), int(num_rows), rows.data_ptr(),
+            rows.shape[0], table, out.data_ptr(), row_list.data_ptr(), row_count.data_ptr())
+    return _LaunchSpec("settle", _lib().gdn_recoverssm_settle, args, dev, keepalive=tuple(held))
+
+
+def _to_device_rows(values: list, device) -> torch.Tensor:
+    """An int32 tensor of the host list ``values`` on ``device``, copied on
+    the current stream from pinned memory without waiting for the device (the
+    pinned staging block is not reused before the copy has run)."""
+    if torch.device(device).type == "cpu":
+        return torch.tensor(values, dtype=torch.int32)
+    return torch.tensor(values, dtype=torch.int32, pin_memory=True).to(device, non_blocking=True)
 
 
 # ---------------------------------------------------------------------------
@@ -699,16 +725,27 @@ def _make_fold_spec(*, pages: LayerPages, record_rows, key_heads, key_dtype, row
     return spec
 
 
-def _fold_rows_spec(spec: _LaunchSpec, rows: torch.Tensor) -> _LaunchSpec:
+def _fold_rows_spec(spec: _LaunchSpec, rows: torch.Tensor, count: torch.Tensor | None = None, *,
+                    lengths: torch.Tensor | None = None, listed: int | None = None) -> _LaunchSpec:
     """The same fold over the listed plan rows only: ``rows`` is a strictly
     increasing int32 tensor on the fold's device (the extension block's row
     list), so the launch has a workgroup per (layer, listed row, head)
-    instead of one per row of the plan."""
+    instead of one per row of the plan. With ``count`` (a device int32 the
+    device wrote) only the first ``count`` of ``listed`` entries (all of
+    ``rows`` by default) are folded, by a fixed grid that loops over their
+    tiles. ``lengths`` replaces the plan's accepted lengths."""
     ext = N.FoldExt.from_buffer_copy(spec.ext)
     ext.row_list = rows.data_ptr()
-    ext.row_list_len = rows.numel()
-    out = _LaunchSpec(spec.name, spec.fn, spec.args[:-1] + (ctypes.byref(ext),), spec.device,
-                      keepalive=spec.keepalive + (rows, ext))
+    ext.row_list_len = rows.numel() if listed is None else int(listed)
+    held = (rows, ext)
+    if count is not None:
+        ext.row_count = count.data_ptr()
+        held += (count,)
+    args = list(spec.args[:-1]) + [ctypes.byref(ext)]
+    if lengths is not None:
+        args[_FOLD_LENGTHS_ARG] = lengths.data_ptr()
+        held += (lengths,)
+    out = _LaunchSpec(spec.name, spec.fn, tuple(args), spec.device, keepalive=spec.keepalive + held)
     out.config, out.ext = spec.config, ext
     return out
 
@@ -716,11 +753,12 @@ def _fold_rows_spec(spec: _LaunchSpec, rows: torch.Tensor) -> _LaunchSpec:
 def _picked_rows(rows, num_rows: int, device) -> torch.Tensor | None:
     """Pending rows named by a flush, checked against the plan's rows, as a
     sorted int32 tensor of distinct rows on ``device`` (None when empty)."""
-    pick = torch.as_tensor(rows, dtype=torch.int64).reshape(-1).cpu()
-    require(bool(((pick >= 0) & (pick < num_rows)).all()), "flushed rows must be rows of the pending plan")
-    if pick.numel() == 0:
+    # Host rows (a list, or a tensor read back once); checked and sorted here.
+    pick = rows.reshape(-1).tolist() if isinstance(rows, torch.Tensor) else [int(r) for r in rows]
+    require(all(0 <= r < num_rows for r in pick), "flushed rows must be rows of the pending plan")
+    if not pick:
         return None
-    return torch.unique(pick).to(torch.int32).to(device)
+    return _to_device_rows(sorted(set(pick)), device)
 
 
 # Positions in the fold's argument tuple: 4 reference tensors, 8 tables,
@@ -806,6 +844,10 @@ class GDNRecoverSSMCommitContext:
         self.__dict__.update(plan)
         # Rows of the next batch continue the same rows of a pending commit.
         self.pending_rows = torch.arange(max_num_reqs, dtype=torch.int32, device=dev)
+        # What a settle folds (settle_deferred): lengths, listed rows, count.
+        self.settle_lens = torch.zeros(max_num_reqs, dtype=torch.int32, device=dev)
+        self.settle_rows = torch.zeros(max(1, max_num_reqs), dtype=torch.int32, device=dev)
+        self.settle_count = torch.zeros(1, dtype=torch.int32, device=dev)
 
     # The reference context's table attributes, served from the bound pages.
     conv_states = property(lambda self: self.pages.conv_states)
@@ -1094,15 +1136,19 @@ class GDNRecoverSSMCommitContext:
         """
         spec = getattr(self, "_deferred_fold", None)
         require(spec is not None, "no deferred commit to flush")
-        num = self._deferred_rows
         rows = self.pending_rows if rows is None else rows
         require(next_state_indices.ndim == 1 and rows.shape[0] >= next_state_indices.shape[0],
                 "the pending row map does not cover the next batch")
-        lengths = _unapplied_lengths(self.commit_lens, self.final_state_indices, num, rows, next_state_indices)
-        args = list(spec.args)
-        args[_FOLD_LENGTHS_ARG] = lengths.data_ptr()
-        spec = _LaunchSpec(spec.name, spec.fn, tuple(args), spec.device, keepalive=spec.keepalive + (lengths,))
-        _submit(spec, _collect)
+        # The device decides which rows to fold and lists them in the
+        # context's own arrays (the plan's lengths stay for the verifies);
+        # the fold then covers the listed rows only.
+        num = self._deferred_rows
+        if num == 0:
+            return  # nothing is pending
+        _submit(_settle_spec(self.commit_lens, self.final_state_indices, self.commit_lens.shape[0], num, rows,
+                             [next_state_indices], self.settle_lens, self.settle_rows, self.settle_count), _collect)
+        _submit(_fold_rows_spec(spec, self.settle_rows, self.settle_count, lengths=self.settle_lens, listed=num),
+                _collect)
 
     def flush_deferred(self, rows: Sequence[int] | torch.Tensor | None = None, _collect: list | None = None) -> None:
         """Apply the last ``commit_deferred`` plan with the ordinary fold.

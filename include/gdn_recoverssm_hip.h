@@ -26,6 +26,8 @@
  *                                   563-568: the fold (csrc/ops.cpp:170-239) applied inside the
  *                                   next step's verify
  *   gdn_recoverssm_set_state_cache_retain -> no counterpart: a cache hint for the verify launches
+ *   gdn_recoverssm_settle        -> no counterpart: which pending rows of a deferred commit a
+ *                                   settle folds (the next verifies do not apply them)
  */
 #ifndef GDN_RECOVERSSM_HIP_H
 #define GDN_RECOVERSSM_HIP_H
@@ -99,10 +101,18 @@ typedef struct gdn_fold_ext {
    * [0, rows) or not greater than the entry before it folds nothing, so no row
    * is ever folded twice. The grid then covers layers x row_list_len x heads
    * instead of every row, which is what a flush of a few rows (requests that
-   * left a deferred batch) costs. */
+   * left a deferred batch) costs. When row_count is not NULL as well (a device
+   * int32 the device wrote, e.g. by gdn_recoverssm_settle), only the first
+   * min(*row_count, row_list_len) entries are folded, by a fixed grid of at
+   * most GDN_FOLD_LISTED_GRID workgroups that take the (layer, listed row,
+   * head) tiles in turn: a list the host cannot size costs the tiles it
+   * names, not a launch over every row. */
   const int32_t *row_list;
   int64_t row_list_len;
+  const int32_t *row_count;
 } gdn_fold_ext;
+
+#define GDN_FOLD_LISTED_GRID 512
 
 int gdn_recoverssm_abi_version(void);
 
@@ -371,6 +381,38 @@ int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_buckets, cons
                            const void *idx_mapping, int32_t idx_mapping_dtype, int64_t idx_mapping_len,
                            int32_t *persistent_cols, int32_t *persistent_accepted, int64_t persistent_len,
                            int64_t num_rows, void *stream);
+
+/* No counterpart in the reference: what a settle of a deferred commit folds,
+ * decided on the device for the 1..GDN_SETTLE_MAX_GROUPS plan groups of one
+ * plan (a commit context, or a bucket of cache groups). Group g's pending row
+ * r < num_rows is applied by the next step's deferred verify when some next
+ * row b < next[g].rows has rows[b] == r and next[g].state_indices[b *
+ * next[g].stride] == finals[g * capacity + r] (the verify's own test). Then
+ * out_lengths[g * capacity + r] = 0 for every applied row and lengths[...]
+ * for every other entry (entries from num_rows on included), and row_list
+ * receives, ascending, every r < num_rows whose out length is above 0 in some
+ * group, *row_count their number: a gdn_recoverssm_fold of out_lengths with
+ * that row list and count (gdn_fold_ext.row_list / row_count) commits
+ * exactly the pending rows the next verifies will not apply. lengths, finals
+ * and out_lengths hold num_groups * capacity entries, row_list at least
+ * max(num_rows, 1), rows (the next batch's row map: next row -> pending row,
+ * -1 for a new request) at least the largest next[g].rows; `next` is a HOST
+ * array of num_groups entries (rows 0: nothing of that group is applied).
+ * One workgroup; num_rows is at most GDN_SETTLE_MAX_ROWS. The outputs share
+ * memory with no input and with each other. */
+#define GDN_SETTLE_MAX_GROUPS 3
+#define GDN_SETTLE_MAX_ROWS 65536
+typedef struct gdn_settle_next {
+  const void *state_indices; /* DEVICE: the next batch's state index of row b at b * stride */
+  int64_t stride;            /* element stride */
+  int64_t rows;              /* next rows of this group */
+  int32_t dtype;             /* GDN_DT_I32 / GDN_DT_I64 */
+  int32_t reserved;
+} gdn_settle_next;
+
+int gdn_recoverssm_settle(const int32_t *lengths, const int32_t *finals, int64_t num_groups, int64_t capacity,
+                          int64_t num_rows, const int32_t *rows, int64_t rows_len, const gdn_settle_next *next,
+                          int32_t *out_lengths, int32_t *row_list, int32_t *row_count, void *stream);
 
 #ifdef __cplusplus
 }

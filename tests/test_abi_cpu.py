@@ -215,6 +215,56 @@ def test_fold_row_list_is_checked_before_launch():
     assert st == N.GDN_ERR_INVALID and b"gdn_recoverssm_fold only" in lib.gdn_recoverssm_last_error()
 
 
+def test_settle_is_checked_before_launch():
+    """gdn_recoverssm_settle refuses 0 or more than 3 groups, pending rows
+    beyond the plan, a row map or index array that does not cover a group's
+    next rows, a non-index dtype and outputs that share memory with an input
+    or with each other, before any HIP call (the addresses are never
+    dereferenced). A fold row count without a row list is refused too."""
+    lib = N.load()
+    L, F, R, X, O, RL, C = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000, 0x70000
+
+    def call(groups=1, nexts=None, **kw):
+        a = dict(lengths=L, finals=F, cap=8, num_rows=4, rows=R, rows_len=6, out=O, rl=RL, cnt=C)
+        a.update(kw)
+        table = (N.SettleNext * max(groups, 1))()
+        for g, n in enumerate(nexts or [dict(state_indices=X, stride=1, rows=6, dtype=N.DT_I32)] * groups):
+            for k, v in n.items():
+                setattr(table[g], k, v)
+        return lib.gdn_recoverssm_settle(a["lengths"], a["finals"], groups, a["cap"], a["num_rows"], a["rows"],
+                                         a["rows_len"], table, a["out"], a["rl"], a["cnt"], None)
+
+    good = dict(state_indices=X, stride=1, rows=6, dtype=N.DT_I32)
+    for kw, msg in [
+        (dict(groups=0), b"groups"),
+        (dict(groups=4), b"groups"),
+        (dict(num_rows=9), b"pending rows"),
+        (dict(num_rows=-1), b"pending rows"),
+        (dict(cap=0, num_rows=0), b"groups"),
+        (dict(out=0), b"missing"),
+        (dict(cnt=0), b"missing"),
+        (dict(rows_len=5), b"cover"),
+        (dict(rows=0), b"cover"),
+        (dict(nexts=[dict(good, state_indices=0)]), b"cover"),
+        (dict(nexts=[dict(good, dtype=N.DT_F32)]), b"cover"),
+        (dict(nexts=[dict(good, stride=-1)]), b"cover"),
+        (dict(nexts=[dict(good, rows=-1)]), b"cover"),
+        (dict(groups=2, nexts=[good, dict(good, rows=7)]), b"group 1"),
+        (dict(out=L + 16), b"output lengths overlaps the plan lengths"),
+        (dict(groups=2, nexts=[good, good], out=F - 32), b"output lengths overlaps the final pages"),
+        (dict(rl=R), b"row list overlaps the row map"),
+        (dict(cnt=X + 8, nexts=[dict(good, dtype=N.DT_I64)]), b"row count overlaps the next state indices"),
+        (dict(rl=O + 28), b"output lengths overlaps the row list"),
+    ]:
+        st = call(**kw)
+        assert st == N.GDN_ERR_INVALID and msg in lib.gdn_recoverssm_last_error(), (kw, lib.gdn_recoverssm_last_error())
+    fcfg = N.i64_array([4, 1, 4, 2, 4, 16, 4, 8, 0, 128 * 128, 128, 512, 128, 256, 128, 4, 1])
+    fext = N.FoldExt(key_dim=128, value_dim=128, state_k_stride=1, source_dtype=3, source_stride=1, row_count=C)
+    st = lib.gdn_recoverssm_fold(None, None, None, None, *([8] * 8), None, *[0x10000, 0x20000, 0x30000, 0x40000,
+                                 0x50000], fcfg, 17, ctypes.byref(fext), None)
+    assert st == N.GDN_ERR_INVALID and b"row count applies to a row list" in lib.gdn_recoverssm_last_error()
+
+
 def test_commit_noalloc_rejects_before_touching_the_device():
     """The no-allocation commit refuses caller plan arrays and a plan larger
     than the library's buffer before any HIP call (none is possible here)."""
@@ -286,7 +336,9 @@ int main(void) {
   F(gdn_gating_ext, softplus_beta) F(gdn_gating_ext, softplus_threshold)
   F(gdn_verify_ext, out_dtype) F(gdn_verify_ext, key_per_value_head)
   F(gdn_fold_ext, source_stride) F(gdn_fold_ext, state_k_stride) F(gdn_fold_ext, row_list)
-  F(gdn_fold_ext, row_list_len)
+  F(gdn_fold_ext, row_list_len) F(gdn_fold_ext, row_count)
+  printf("gdn_settle_next %zu\n", sizeof(gdn_settle_next));
+  F(gdn_settle_next, stride) F(gdn_settle_next, rows) F(gdn_settle_next, dtype)
   F(gdn_plan_group, block_table) F(gdn_plan_group, table_rows) F(gdn_plan_group, num_computed)
   F(gdn_plan_group, computed_dtype) F(gdn_plan_group, num_blocks) F(gdn_plan_group, block_size)
   return 0;
@@ -309,6 +361,7 @@ def test_ctypes_struct_layout_matches_c_compiler():
     assert int(got["gdn_pending_commit"]) == ctypes.sizeof(N.PendingCommit)
     assert int(got["gdn_plan_launch"]) == ctypes.sizeof(N.PlanLaunch)
     assert int(got["gdn_conv_launch"]) == ctypes.sizeof(N.ConvLaunch)
+    assert int(got["gdn_settle_next"]) == ctypes.sizeof(N.SettleNext)
     assert int(got.pop("noalloc_entries")) == N.NOALLOC_PLAN_ENTRIES
     for key, value in got.items():
         if "." not in key:
@@ -316,7 +369,8 @@ def test_ctypes_struct_layout_matches_c_compiler():
         struct, fld = key.split(".")
         cls = {"gdn_verify_ext": N.VerifyExt, "gdn_fold_ext": N.FoldExt, "gdn_plan_group": N.PlanGroup,
                "gdn_gating_ext": N.GatingExt, "gdn_pending_commit": N.PendingCommit,
-               "gdn_plan_launch": N.PlanLaunch, "gdn_conv_launch": N.ConvLaunch}[struct]
+               "gdn_plan_launch": N.PlanLaunch, "gdn_conv_launch": N.ConvLaunch,
+               "gdn_settle_next": N.SettleNext}[struct]
         assert getattr(cls, fld).offset == int(value), key
 
 

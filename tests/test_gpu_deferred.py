@@ -32,6 +32,7 @@ from gdn_recoverssm_ascend.kernels import (
     GDNRecoverSSMCommitContext,
     ReplayRecordBuffers,
     _fold_rows_spec,
+    _settle_spec,
     continue_pending,
     gdn_recoverssm_verify,
     gdn_recoverssm_verify_deferred,
@@ -577,6 +578,142 @@ def test_settle_folds_what_the_verify_does_not_apply(dev):
         i = inputs1[layer]
         r1 = O.oracle_verify(i.q, i.k, i.v, i.g, i.beta, want[layer], qsl1, idx1, Q)
         _check_verify(outs[layer], recs[1][layer], r1, f"step 1 layer {layer}")
+
+
+def _settle(dev, lengths, finals, cap, num_rows, rows, nexts):
+    """gdn_recoverssm_settle on the GPU for len(nexts) groups of `cap` plan
+    rows; its outputs start poisoned. Returns (lengths, listed rows)."""
+    lengths_d, finals_d = lengths.to(dev), finals.to(dev)
+    out = torch.full(lengths.shape, -7, dtype=torch.int32, device=dev)
+    rl = torch.full((max(num_rows, 1),), -9, dtype=torch.int32, device=dev)
+    cnt = torch.full((1,), -5, dtype=torch.int32, device=dev)
+    nexts_d = [None if x is None else x.to(dev) for x in nexts]
+    _settle_spec(lengths_d, finals_d, cap, num_rows, rows.to(dev), nexts_d, out, rl, cnt).launch()
+    torch.cuda.synchronize()
+    assert torch.equal(lengths_d.cpu(), lengths), "the plan's lengths are not modified"
+    n = int(cnt.cpu())
+    assert 0 <= n <= num_rows
+    return out.cpu(), rl.cpu()[:n]
+
+
+def _settled_by_definition(lengths, finals, cap, num_rows, rows, nexts):
+    """Group g's pending row r < num_rows keeps its length unless some next
+    row b has rows[b] == r and nexts[g][b] == its final page; entries past
+    num_rows are kept. The listed rows: every r < num_rows with a length
+    left in some group, ascending."""
+    out = lengths.clone()
+    for g, nxt in enumerate(nexts):
+        if nxt is None:
+            continue
+        pairs = set(zip(rows[:nxt.shape[0]].tolist(), nxt.tolist()))  # (rows[b], nxt[b]) over the next rows
+        for r in range(num_rows):
+            if (r, int(finals[g * cap + r])) in pairs:
+                out[g * cap + r] = 0
+    listed = [r for r in range(num_rows) if any(int(out[g * cap + r]) > 0 for g in range(len(nexts)))]
+    return out, listed
+
+
+def test_settle_known_cases(dev):
+    """What a settle folds, for hand-made batches: next row 0 continues
+    pending row 2 on its final page (applied), next row 1 continues pending
+    row 0 on another page (not applied), next row 2 is a new request, next
+    row 3 applies pending row 3, pending row 1 left; the entry past the
+    pending rows keeps its length and is not listed."""
+    i32 = torch.int32
+    lengths = torch.tensor([3, 2, 1, 4, 7], dtype=i32)
+    finals = torch.tensor([10, 11, 12, 13, 14], dtype=i32)
+    rows = torch.tensor([2, 0, -1, 3], dtype=i32)
+    nxt = torch.tensor([12, 99, 5, 13], dtype=i32)
+    out, listed = _settle(dev, lengths, finals, 5, 4, rows, [nxt])
+    assert out.tolist() == [3, 2, 0, 0, 7] and listed.tolist() == [0, 1]
+    # an empty next batch applies nothing; a zero length is not listed
+    lengths0 = torch.tensor([3, 0, 1, 4, 7], dtype=i32)
+    out, listed = _settle(dev, lengths0, finals, 5, 5, torch.tensor([-1], dtype=i32), [torch.zeros(0, dtype=i32)])
+    assert out.tolist() == [3, 0, 1, 4, 7] and listed.tolist() == [0, 2, 3, 4]
+    # a row map longer than the batch: only the batch's rows count; a row
+    # index past the pending rows names no pending row (entry 4 is row 4,
+    # past num_rows = 4, whose next index equals its final page)
+    out, listed = _settle(dev, lengths, finals, 5, 4, torch.tensor([4, 1, 0, 2], dtype=i32),
+                          [torch.tensor([14, 11], dtype=torch.int64)])
+    assert out.tolist() == [3, 0, 1, 4, 7] and listed.tolist() == [0, 2, 3]
+    # next state indices as a column of an int64 table (element stride 3)
+    table = torch.tensor([[12, 0, 0], [99, 0, 0], [5, 0, 0], [13, 0, 0]], dtype=torch.int64)
+    out, listed = _settle(dev, lengths, finals, 5, 4, rows, [table[:, 0]])
+    assert out.tolist() == [3, 2, 0, 0, 7] and listed.tolist() == [0, 1]
+    # two groups (plan rows g * 5 + r), a row listed when either group keeps
+    # a length; a third group outside the next step keeps every length
+    lengths3 = torch.cat([lengths, torch.tensor([0, 5, 6, 2, 1], dtype=i32), torch.tensor([1, 1, 0, 0, 9], dtype=i32)])
+    finals3 = torch.cat([finals, torch.tensor([20, 21, 22, 23, 24], dtype=i32), finals])
+    out, listed = _settle(dev, lengths3, finals3, 5, 4, rows,
+                          [nxt, torch.tensor([22, 20, 9, 23], dtype=i32), None])
+    assert out.tolist() == [3, 2, 0, 0, 7, 0, 5, 0, 0, 1, 1, 1, 0, 0, 9]
+    assert listed.tolist() == [0, 1]
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_settle_random_batches(dev, seed):
+    """Seeded batches, from a few rows to several times the kernel's 1024
+    threads (plan, pending rows and next batch), 1-3 groups (some outside the
+    next step), int32 or int64 next indices, contiguous or a strided column:
+    lengths and listed rows equal the definition, row by row."""
+    gen = torch.Generator().manual_seed(100 + seed)
+    cap = [5, 300, 1500, 4000, 3000][seed % 5]
+    groups = 1 + seed % 3
+    num_rows = int(torch.randint(0, cap + 1, (1,), generator=gen))
+    lengths = torch.randint(0, 5, (groups * cap,), generator=gen, dtype=torch.int32)
+    finals = torch.randint(1, 50, (groups * cap,), generator=gen, dtype=torch.int32)
+    nb = int(torch.randint(0, 2 * cap + 1, (1,), generator=gen))
+    rows = torch.randint(-1, cap + 3, (nb + 3,), generator=gen, dtype=torch.int32)
+    nexts = []
+    for g in range(groups):
+        if g == 2 and seed % 2:
+            nexts.append(None)
+            continue
+        own = finals[g * cap + rows[:nb].clamp(0, cap - 1).long()]
+        nxt = torch.where(torch.rand(nb, generator=gen) < 0.6, own,
+                          torch.randint(1, 50, (nb,), generator=gen, dtype=torch.int32))
+        if (seed + g) % 2:
+            nxt = torch.stack([nxt.long(), torch.zeros_like(nxt.long())], 1)[:, 0]  # int64, stride 2
+        nexts.append(nxt)
+    print(f"settle seed {seed}: {groups} groups of {cap}, pending {num_rows}, next {nb}", flush=True)
+    out, listed = _settle(dev, lengths, finals, cap, num_rows, rows, nexts)
+    want, want_listed = _settled_by_definition(lengths, finals, cap, num_rows, rows, nexts)
+    assert torch.equal(out, want), seed
+    assert listed.tolist() == want_listed, seed
+
+
+def test_counted_row_list_folds_the_counted_rows(dev):
+    """A fold with a device row count (gdn_fold_ext.row_count) folds the
+    first `count` entries of its row list, clamped to the list: count 2 of a
+    list of 3 folds two rows, a count past the list folds the whole list,
+    count 0 nothing. Pages equal the oracle's fold of those rows; every other
+    page is unchanged."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=45)
+    s = w.spec
+    L, B, Q = s.layers, s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[2::4] = 2
+    st = _first_step(w, dev, acc)
+    plan, ctx, ckpts = st["plan"], st["ctx"], st["ckpts"]
+    n = plan["commit_lens"]
+    active = [r for r in range(B) if int(n[r]) > 0]
+    assert len(active) >= 7
+    lists = torch.tensor([active[0], active[2], active[4], active[5], active[6]], dtype=torch.int32, device=dev)
+    before = [x.cpu() for x in w.checkpoints]
+    folded = []
+    for entries, count in ((lists[:3], 2), (lists[3:5], 7), (lists[3:5], 0)):
+        print(f"counted fold: rows {entries.tolist()}, count {count}", flush=True)
+        cnt = torch.tensor([count], dtype=torch.int32, device=dev)
+        _fold_rows_spec(ctx._deferred_fold, entries, cnt, listed=entries.numel()).launch()
+        folded += entries.tolist()[:count]
+    torch.cuda.synchronize()
+    lengths = torch.zeros_like(n)
+    lengths[folded] = n[folded]
+    want = _oracle_fold(before, st["results"], plan, B, w.num_pages, lengths=lengths)
+    touched = _touched(dict(plan, commit_lens=lengths), B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the counted folds")
 
 
 def test_rows_past_the_pending_plan_do_not_apply(dev):
