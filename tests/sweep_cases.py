@@ -87,7 +87,8 @@ def deferred_case(i: int) -> dict:
                 rows=rng.randint(2, 12), layers=rng.randint(1, 3), steps=rng.randint(2, 4),
                 block_size=rng.choice([b for b in (4, 8, 16) if b >= Q]),  # a block covers one window
                 seed=rng.randint(0, 10_000),
-                empty_row=rng.random() < 0.3)
+                empty_row=rng.random() < 0.3,
+                move=rng.random() < 0.5)
 
 
 def coordinator_case(i: int) -> dict:

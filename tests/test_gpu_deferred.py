@@ -218,7 +218,11 @@ def test_deferred_step_without_tokens(dev):
     _run_against_oracle(w, dev, acc_steps, qsl_steps)
 
 
-def _flow(w, dev, acc_steps, qsl_steps, *, deferred):
+def _flow(w, dev, acc_steps, qsl_steps, *, deferred, settle=False, move=None):
+    """Verify + commit over the steps, ordinary or deferred. ``settle``: the
+    deferred flow settles before every verify after the first step.
+    ``move`` = (step, row, page): before that step's verifies the row's
+    state index becomes `page` (a page no row uses), in both flows."""
     s = w.spec
     L, B, Q, H, HV, K, V = s.layers, s.rows, s.window, s.key_heads, s.value_heads, s.key_dim, s.value_dim
     wd = w.to(dev)
@@ -235,6 +239,10 @@ def _flow(w, dev, acc_steps, qsl_steps, *, deferred):
     for step, (acc, qsl) in enumerate(zip(acc_steps, qsl_steps)):
         i = step % 2
         qsl = qsl.to(dev)
+        if move is not None and move[0] == step:
+            state_idx[move[1]] = move[2]
+        if deferred and settle and pending is not None:
+            ctxs[1 - i].settle_deferred(state_idx, pending[0].rows)
         outs = []
         for layer in range(L):
             T = int(qsl[-1])
@@ -345,8 +353,10 @@ def test_deferred_commit_equals_ordinary_flow_shapes(dev, K, V, Q, H, HV, act, s
 def test_random_deferred_flows(dev, case):
     """Seeded draws of the deferred flow's options together (head dims, GQA
     ratio, window, activation and state dtypes, rows, layers, steps, block
-    size, a step in which one row has no token): the deferred flow equals the
-    ordinary flow bit for bit, step by step, and after the final flush."""
+    size, a step in which one row has no token, a row given another page
+    before a later step): the deferred flow, settling before every verify
+    after the first step, equals the ordinary flow bit for bit, step by step,
+    and after the final flush."""
     c = SC.deferred_case(case)
     print(f"deferred sweep case {case}: {c}", flush=True)
     w = W.make_workload("decode_loop_l48", layers=c["layers"], rows=c["rows"], key_heads=c["H"],
@@ -364,8 +374,17 @@ def test_random_deferred_flows(dev, case):
         q2 = torch.zeros(s.rows + 1, dtype=torch.int32)
         q2[1:] = torch.cumsum(lens, 0)
         qsl_steps[-1] = q2
-    ref = _flow(w, dev, acc_steps, qsl_steps, deferred=False)
-    _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True))
+    move = None
+    if c["move"]:
+        # a continued request given another page before a later step: a page
+        # of the padded row's table, which no row reads or writes
+        pad = int(w.extras["padded_rows"][0])
+        pages = [int(p) for p in w.meta.block_table[pad].tolist() if 0 < int(p) < w.num_pages]
+        rows = [r for r in range(s.rows) if r != pad]
+        move = (1 + case % (c["steps"] - 1), rows[case % len(rows)], pages[0])
+    print(f"deferred sweep case {case}: move {move}", flush=True)
+    ref = _flow(w, dev, acc_steps, qsl_steps, deferred=False, move=move)
+    _assert_flows_equal(ref, _flow(w, dev, acc_steps, qsl_steps, deferred=True, settle=True, move=move))
 
 
 def _first_step(w, dev, acc):
