@@ -77,16 +77,6 @@ struct VerifyArgs {
   int32_t nt_rows;  // rows b < nt_rows read their state non-temporally
 };
 
-#ifndef GDN_V_STORE_END
-#define GDN_V_STORE_END 0
-#endif
-#ifndef GDN_V_POL_OUT
-#define GDN_V_POL_OUT 0
-#endif
-#ifndef GDN_V_POL_REC
-#define GDN_V_POL_REC 0
-#endif
-
 constexpr int kVerifyThreads = 64;  // one wave per (row, value head, tile)
 constexpr int kTileRows = 128;     // eight MFMA row blocks of 16 rows
 // The deferred-commit kernels stream half tiles: a wave that also stores the
@@ -796,13 +786,12 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
       const bool st = ((valid_mask >> t) & 1u) && row_ok;
       const int oel = t * int(a.out_ts) + lrow;
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res_o[half][t]), rout,
-                                            st && out_f32 ? oel * 4 : kOutOfRange, 0, GDN_V_POL_OUT);
+                                            st && out_f32 ? oel * 4 : kOutOfRange, 0, 0);
       if constexpr (sizeof(A) == 2)
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f32<A>(res_o[half][t])), rout,
-                                              st && !out_f32 ? oel * AS : kOutOfRange, 0, GDN_V_POL_OUT);
+                                              st && !out_f32 ? oel * AS : kOutOfRange, 0, 0);
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res_c[half][t]), rcorr,
-                                            st && rec_ok ? (t * a.corr_ts + lrow) * 4 : kOutOfRange, 0,
-                                            GDN_V_POL_REC);
+                                            st && rec_ok ? (t * a.corr_ts + lrow) * 4 : kOutOfRange, 0, 0);
     }
   };
   auto recurrence = [&](int half) {
@@ -827,7 +816,7 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
       res_c[half][t] = c;
       res_o[half][t] = wq[t];
     }
-    if (!GDN_V_STORE_END) emit(half);
+    emit(half);
     wave_lds_sync();  // d_lds may be overwritten by the next half
   };
 #pragma unroll
@@ -865,10 +854,6 @@ __device__ __forceinline__ void verify_wave(const VerifyArgs &a, VerifyLds<QM, 4
     // Every half runs its recurrence, also one past V (its rows store nothing):
     // skipping it would be a path without its stores.
     if ((rb + 2) % 4 == 0) recurrence((rb + 2) / 4 - 1);
-  }
-  if (GDN_V_STORE_END) {
-#pragma unroll
-    for (int half = 0; half < NRB / 4; ++half) emit(half);
   }
 }
 
