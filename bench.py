@@ -914,12 +914,12 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
     torch.cuda.synchronize()
     verify_ms = sum(timer.elapsed(a, b) for a, b, _ in ev) / steps
     commit_ms = sum(timer.elapsed(b, c) for _, b, c in ev) / steps
-    settle_us = flush_us = None
+    settle_us = settle_left_us = flush_us = None
     if coord is not None and deferred:
         # Every row here continues on its final page, so no step needs a
         # settle; a serving loop whose batch changes calls it (or flush(rows))
-        # before the verifies: its cost with nothing to fold, one fold launch
-        # per bucket over every row.
+        # before the verifies. Its cost with nothing to fold: per bucket the
+        # settle kernel and a fold over the rows it lists (none here).
         # The next step's metadata (the last step's carried forward): every
         # pending row continues on its final page. The first call loads its
         # kernels; timed are the calls after it.
@@ -934,14 +934,35 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
         timer.record(s1)
         torch.cuda.synchronize()
         settle_us = timer.elapsed(s0, s1) / 5 * 1e3
-        # What a step whose batch lost two requests pays instead: their
-        # pending commits folded through the fold's row list (timing only:
-        # the same two rows folded again each call).
-        deferred_step[1].flush(rows=[0, 1])
+        # What a step whose batch lost two requests pays: a settle whose row
+        # map gives those two rows' slots to new requests (it folds their
+        # pending commits through the counted row list), and, instead, a
+        # flush of two given rows. Both mark what they fold, so every call
+        # takes two other committed rows (the first of each kind loads its
+        # kernels; timed are the five after it); the row maps are built
+        # before the timed calls.
+        committed = [r for r, n in enumerate(deferred_step[1]._plan(0)[1][:B].tolist()) if n > 0]
+        pairs = [committed[2 * k:2 * k + 2] for k in range(12)]
+        maps = []
+        for pair in pairs[:6]:
+            mp = torch.arange(B, dtype=torch.int32)
+            mp[pair] = -1
+            maps.append(mp.to(dev))
+        deferred_step[1].rows = maps[0]
+        deferred_step[1].settle(metas[0])
         torch.cuda.synchronize()
         timer.record(s0)
-        for _ in range(5):
-            deferred_step[1].flush(rows=[0, 1])
+        for mp in maps[1:]:
+            deferred_step[1].rows = mp
+            deferred_step[1].settle(metas[0])
+        timer.record(s1)
+        torch.cuda.synchronize()
+        settle_left_us = timer.elapsed(s0, s1) / 5 * 1e3
+        deferred_step[1].flush(rows=pairs[6])
+        torch.cuda.synchronize()
+        timer.record(s0)
+        for pair in pairs[7:]:
+            deferred_step[1].flush(rows=pair)
         timer.record(s1)
         torch.cuda.synchronize()
         flush_us = timer.elapsed(s0, s1) / 5 * 1e3
@@ -991,6 +1012,7 @@ def _run_decode_loop(name, *, deferred, steps=None, warmup=10, groups=None):
         line["launches_per_commit"] = coord.last_launch_count
     if settle_us is not None:
         line["settle_us"] = round(settle_us, 1)
+        line["settle_two_left_us"] = round(settle_left_us, 1)
         line["flush_two_rows_us"] = round(flush_us, 1)
     if deferred:
         # The step's state reads that the deferred commit removes: one page read
@@ -1030,6 +1052,7 @@ def decode_loop_summary(warmup):
             entry["launches_per_commit"] = line["launches_per_commit"]
             if "settle_us" in line:
                 entry["settle_us"] = line["settle_us"]
+                entry["settle_two_left_us"] = line["settle_two_left_us"]
                 entry["flush_two_rows_us"] = line["flush_two_rows_us"]
         entry["gbs"] = entry.pop("value")
         if deferred:
@@ -1051,9 +1074,10 @@ def decode_loop_summary(warmup):
                    "(the deferred verify reads every row non-temporally); coordinator_*: the same loop committed "
                    f"through GroupedCommitCoordinator with the layers in {LOOP_GROUPS} cache groups (two buckets "
                    "and the publication across them); no request leaves, so the deferred loop needs no settle "
-                   "(settle_us: one settle with nothing to fold; flush_two_rows_us: the commits of two rows "
-                   "folded across every layer through the fold's row list, what a batch that loses two "
-                   "requests pays)")
+                   "(settle_us: one settle with nothing to fold; settle_two_left_us: one settle after two "
+                   "requests left, folding their commits across every layer through the counted row list; "
+                   "flush_two_rows_us: the same two rows' commits folded by a flush through the fold's row "
+                   "list instead)")
     return res
 
 

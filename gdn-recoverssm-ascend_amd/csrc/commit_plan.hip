@@ -169,9 +169,11 @@ __global__ __launch_bounds__(64) void publish_kernel(const int64_t *__restrict__
 // group has rows[b] == r and b's next state index is r's final page (the
 // test by which the deferred verify applies a pending commit); the applied
 // rows are marked in an LDS bitmap first, so every output entry is then
-// written once: 0 for an applied row, the plan's length otherwise. The rows
-// left with a length in some group are listed in ascending order (a prefix
-// sum over each tile of 1024 rows), and their number stored last.
+// written once: 0 for an applied row, the plan's length otherwise. The plan's
+// length of every entry handed to the fold becomes 0 (each entry is read and
+// written by one thread), so a later settle or flush does not fold it again.
+// The rows left with a length in some group are listed in ascending order (a
+// prefix sum over each tile of 1024 rows), and their number stored last.
 constexpr int kSettleThreads = 1024;
 constexpr int kSettleWaves = kSettleThreads / 64;
 
@@ -182,7 +184,7 @@ struct SettleNext {
   int32_t dtype[GDN_SETTLE_MAX_GROUPS];
 };
 
-__global__ __launch_bounds__(kSettleThreads) void settle_kernel(const int32_t *__restrict__ lengths,
+__global__ __launch_bounds__(kSettleThreads) void settle_kernel(int32_t *__restrict__ lengths,
                                                                 const int32_t *__restrict__ finals, int32_t groups,
                                                                 int64_t cap, int32_t num_rows,
                                                                 const int32_t *__restrict__ rows, SettleNext nx,
@@ -215,7 +217,10 @@ __global__ __launch_bounds__(kSettleThreads) void settle_kernel(const int32_t *_
         const bool hit = r < num_rows && ((applied[g][r >> 5] >> (r & 31)) & 1u);
         const int32_t n = hit ? 0 : lengths[i];
         out[i] = n;
-        left = left || (r < num_rows && n > 0);
+        if (r < num_rows && n > 0) {
+          lengths[i] = 0;  // folded by this settle's fold
+          left = true;
+        }
       }
     }
     const uint64_t m = __ballot(left);
@@ -546,7 +551,7 @@ extern "C" int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_bu
   return GDN_OK;
 }
 
-extern "C" int gdn_recoverssm_settle(const int32_t *lengths, const int32_t *finals, int64_t num_groups,
+extern "C" int gdn_recoverssm_settle(int32_t *lengths, const int32_t *finals, int64_t num_groups,
                                      int64_t capacity, int64_t num_rows, const int32_t *rows, int64_t rows_len,
                                      const gdn_settle_next *next, int32_t *out_lengths, int32_t *row_list,
                                      int32_t *row_count, void *stream) {

@@ -26,7 +26,7 @@ from . import _native as N
 from ._rules import enforce, fail, require
 from ._tables import LayerPages
 from .kernels import (_FOLD_LENGTHS_ARG, NULL_BLOCK_ID, PendingCommit, _conv_spec, _fill_plan_group,
-                      _fold_rows_spec, _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _picked_rows,
+                      _fold_rows_spec, _fuse_plan_fold, _LaunchSpec, _make_fold_spec, _MarkFolded, _picked_rows,
                       _request_row_map, _settle_spec)
 
 logger = logging.getLogger("gdn_recoverssm_ascend.grouped_commit")
@@ -296,7 +296,9 @@ class DeferredGroupedCommit:
     request. Every pending row must be folded once before its pages are
     reused: by the next verify that continues it, or here, by ``settle``
     (every row the next verifies will not apply, decided on the device) or
-    ``flush`` (given rows, or all). The object stays valid until the same
+    ``flush`` (given rows, or all). Both mark what they fold in the plan, so
+    a later settle or flush skips it; a row a verify has applied must not be
+    flushed. The object stays valid until the same
     contexts commit again (their plan arrays are reused then): a deferred
     flow alternates two sets of contexts, as the pending step's records must
     not be the ones the next verify writes.
@@ -345,7 +347,9 @@ class DeferredGroupedCommit:
 
     def flush(self, rows=None) -> None:
         """Fold the given pending rows (every planned row when None) of every
-        group now, with the ordinary fold."""
+        group now, with the ordinary fold, and mark them folded in the plan
+        (accepted length 0), so a later flush or settle does not fold them
+        again."""
         picked = None
         if rows is not None:
             picked = _picked_rows(rows, self.num_rows, self.rows.device)
@@ -354,10 +358,12 @@ class DeferredGroupedCommit:
         for bucket, fold, _ in self._buckets():
             if picked is None:
                 self._fold(bucket, fold, bucket.length)
+                _MarkFolded(bucket.length, bucket.capacity, num_rows=self.num_rows).launch()
             else:
                 # Every group of a bucket is a member of the step: the row list
                 # folds the picked rows of each (plan row g * capacity + r).
                 _fold_rows_spec(fold, picked).launch()
+                _MarkFolded(bucket.length, bucket.capacity, picked).launch()
 
     def settle(self, next_metadata) -> None:
         """Fold now every pending row that the next step's deferred verifies
@@ -370,9 +376,10 @@ class DeferredGroupedCommit:
         if self.num_rows == 0:
             return  # nothing is pending
         for bucket, fold, members in self._buckets():
-            # The device decides which rows to fold and lists them in the
-            # bucket's own arrays (the plan's lengths stay for the verifies),
-            # one launch for its groups; the fold covers the listed rows only.
+            # The device decides which rows to fold, lists them in the
+            # bucket's own arrays and marks them folded in the plan (the rows
+            # the verifies apply keep their lengths), one launch for its
+            # groups; the fold covers the listed rows only.
             nexts = [None] * (bucket.length.shape[0] // bucket.capacity)
             for i, g in members:
                 nexts[g] = nxt[i].payload.state_indices

@@ -612,8 +612,9 @@ def _settle_spec(lengths: torch.Tensor, finals: torch.Tensor, capacity: int, num
     final page (the deferred verify's own test); ``out`` gets the plan's
     lengths with 0 for the applied rows, ``row_list`` / ``row_count`` the
     ascending rows left with a length in some group and their number, for a
-    fold over them (``_fold_rows_spec``). Nothing is synchronised with the
-    host."""
+    fold over them (``_fold_rows_spec``); the plan's length of every entry
+    handed on that way becomes 0, so a later settle or flush does not fold it
+    again. Nothing is synchronised with the host."""
     groups = len(nexts)
     require(1 <= groups <= N.SETTLE_MAX_GROUPS, f"a settle covers 1..{N.SETTLE_MAX_GROUPS} plan groups")
     require(0 <= num_rows <= min(capacity, N.SETTLE_MAX_ROWS),
@@ -637,6 +638,28 @@ def _settle_spec(lengths: torch.Tensor, finals: torch.Tensor, capacity: int, num
     args = (lengths.data_ptr(), finals.data_ptr(), groups, int(capacity), int(num_rows), rows.data_ptr(),
             rows.shape[0], table, out.data_ptr(), row_list.data_ptr(), row_count.data_ptr())
     return _LaunchSpec("settle", _lib().gdn_recoverssm_settle, args, dev, keepalive=tuple(held))
+
+
+class _MarkFolded:
+    """After an explicit fold of pending rows (a flush), their accepted
+    lengths in the plan become 0, so a later flush or settle of the same plan
+    folds them no more; launched in stream order, like a ``_LaunchSpec``.
+    ``lengths`` holds ``groups`` plan groups of ``capacity`` rows; ``rows``
+    (a device int32 tensor) names the folded rows of every group, None the
+    first ``num_rows`` of each."""
+
+    name = "mark_folded"
+
+    def __init__(self, lengths: torch.Tensor, capacity: int, rows: torch.Tensor | None = None, num_rows: int = 0):
+        self.view = lengths.view(-1, int(capacity))
+        self.rows = None if rows is None else rows.long()
+        self.num_rows = int(num_rows)
+
+    def launch(self) -> None:
+        if self.rows is None:
+            self.view[:, :self.num_rows].zero_()
+        else:
+            self.view.index_fill_(1, self.rows, 0)
 
 
 def _to_device_rows(values: list, device) -> torch.Tensor:
@@ -1139,9 +1162,9 @@ class GDNRecoverSSMCommitContext:
         rows = self.pending_rows if rows is None else rows
         require(next_state_indices.ndim == 1 and rows.shape[0] >= next_state_indices.shape[0],
                 "the pending row map does not cover the next batch")
-        # The device decides which rows to fold and lists them in the
-        # context's own arrays (the plan's lengths stay for the verifies);
-        # the fold then covers the listed rows only.
+        # The device decides which rows to fold, lists them in the context's
+        # own arrays and marks them folded in the plan (the rows the verifies
+        # apply keep their lengths); the fold then covers the listed rows only.
         num = self._deferred_rows
         if num == 0:
             return  # nothing is pending
@@ -1156,8 +1179,10 @@ class GDNRecoverSSMCommitContext:
         ``rows=None`` folds every planned row (a step that runs no verify
         after it, e.g. the end of a batch); a list of pending rows folds only
         those (rows whose request left the batch, see ``continue_pending``),
-        leaving the rest to the next verify. A row must be folded once: by a
-        flush or by the verify that continues it, never both.
+        leaving the rest to the next verify. The folded rows are then marked
+        in the plan (accepted length 0), so a later flush or settle does not
+        fold them again; a row the next verify has applied is not marked
+        (every layer's verify reads the plan), so it must not be flushed.
         """
         spec = getattr(self, "_deferred_fold", None)
         require(spec is not None, "no deferred commit to flush")
@@ -1167,10 +1192,11 @@ class GDNRecoverSSMCommitContext:
             if picked is None:
                 return
             spec = _fold_rows_spec(spec, picked)
-        if _collect is not None:
-            _collect.append(spec)
+            mark = _MarkFolded(self.commit_lens, self.commit_lens.shape[0], picked)
         else:
-            spec.launch()
+            mark = _MarkFolded(self.commit_lens, self.commit_lens.shape[0], num_rows=self._deferred_rows)
+        _submit(spec, _collect)
+        _submit(mark, _collect)
 
 
 __all__ = [

@@ -393,7 +393,10 @@ int gdn_recoverssm_publish(const int64_t *descriptors, int64_t num_buckets, cons
  * receives, ascending, every r < num_rows whose out length is above 0 in some
  * group, *row_count their number: a gdn_recoverssm_fold of out_lengths with
  * that row list and count (gdn_fold_ext.row_list / row_count) commits
- * exactly the pending rows the next verifies will not apply. lengths, finals
+ * exactly the pending rows the next verifies will not apply. The plan's
+ * length of every entry handed on that way (r < num_rows, out length above
+ * 0) is set to 0, so a later settle or flush of the same plan does not fold
+ * it again, while the rows the verifies apply keep theirs. lengths, finals
  * and out_lengths hold num_groups * capacity entries, row_list at least
  * max(num_rows, 1), rows (the next batch's row map: next row -> pending row,
  * -1 for a new request) at least the largest next[g].rows; `next` is a HOST
@@ -410,7 +413,7 @@ typedef struct gdn_settle_next {
   int32_t reserved;
 } gdn_settle_next;
 
-int gdn_recoverssm_settle(const int32_t *lengths, const int32_t *finals, int64_t num_groups, int64_t capacity,
+int gdn_recoverssm_settle(int32_t *lengths, const int32_t *finals, int64_t num_groups, int64_t capacity,
                           int64_t num_rows, const int32_t *rows, int64_t rows_len, const gdn_settle_next *next,
                           int32_t *out_lengths, int32_t *row_list, int32_t *row_count, void *stream);
 

@@ -609,10 +609,17 @@ def _settle(dev, lengths, finals, cap, num_rows, rows, nexts):
     nexts_d = [None if x is None else x.to(dev) for x in nexts]
     _settle_spec(lengths_d, finals_d, cap, num_rows, rows.to(dev), nexts_d, out, rl, cnt).launch()
     torch.cuda.synchronize()
-    assert torch.equal(lengths_d.cpu(), lengths), "the plan's lengths are not modified"
     n = int(cnt.cpu())
     assert 0 <= n <= num_rows
-    return out.cpu(), rl.cpu()[:n]
+    got = out.cpu()
+    # the plan keeps every length except those handed to the fold (marked 0)
+    marked = lengths.clone()
+    for g in range(len(nexts)):
+        for r in range(num_rows):
+            if int(got[g * cap + r]) > 0:
+                marked[g * cap + r] = 0
+    assert torch.equal(lengths_d.cpu(), marked), "the plan's lengths after the settle"
+    return got, rl.cpu()[:n]
 
 
 def _settled_by_definition(lengths, finals, cap, num_rows, rows, nexts):
@@ -699,6 +706,48 @@ def test_settle_random_batches(dev, seed):
     want, want_listed = _settled_by_definition(lengths, finals, cap, num_rows, rows, nexts)
     assert torch.equal(out, want), seed
     assert listed.tolist() == want_listed, seed
+
+
+def test_flushes_and_settles_fold_each_row_once(dev):
+    """A settle or a flush marks what it folds in the plan, so repeated and
+    mixed calls fold every pending row once: a flush of row a, a flush of a
+    and b, a settle in which a and b left and row c was given another page
+    (folding c), the same settle again, then a flush of everything (the rows
+    no verify has applied). The pages then equal the oracle's fold of the
+    whole step, each commit applied once."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=47)
+    s = w.spec
+    L, B, Q = s.layers, s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[1::3] = 2
+    st = _first_step(w, dev, acc)
+    plan, ctx, ckpts = st["plan"], st["ctx"], st["ckpts"]
+    n, fin = plan["commit_lens"], plan["final"]
+    active = [r for r in range(B) if int(n[r]) > 0]
+    assert len(active) >= 3
+    a, b, c = active[0], active[1], active[2]
+    pad = int(w.extras["padded_rows"][0])
+    free_page = next(int(p) for p in w.meta.block_table[pad].tolist() if 0 < int(p) < w.num_pages)
+    print(f"fold once: rows a={a} b={b} c={c}, c moves to page {free_page}", flush=True)
+    before = [x.cpu() for x in w.checkpoints]
+    ctx.flush_deferred(rows=[a])
+    ctx.flush_deferred(rows=[a, b])
+    # the next batch: a and b replaced by new requests, c on another page,
+    # every other row on its final page
+    rows = torch.arange(B, dtype=torch.int32)
+    rows[a] = rows[b] = -1
+    nxt = torch.where(n > 0, fin, torch.zeros_like(fin)).to(torch.int32)
+    nxt[c] = free_page
+    ctx.settle_deferred(nxt.to(dev), rows.to(dev))
+    ctx.settle_deferred(nxt.to(dev), rows.to(dev))
+    ctx.flush_deferred()
+    torch.cuda.synchronize()
+    assert int(ctx.commit_lens[:B].cpu().abs().sum()) == 0, "every pending row is marked folded"
+    want = _oracle_fold(before, st["results"], plan, B, w.num_pages)
+    touched = _touched(plan, B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the flushes and settles")
 
 
 def test_counted_row_list_folds_the_counted_rows(dev):
