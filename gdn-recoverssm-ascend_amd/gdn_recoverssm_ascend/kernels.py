@@ -459,7 +459,9 @@ class PendingCommit:
     """One layer's commit left for the next verify (``gdn_recoverssm_verify_deferred``).
 
     ``rows`` (int32, one entry per row of the next batch) names the pending
-    row each next row continues, -1 for none. The plan arrays (source page,
+    row each next row continues, -1 for none; no two next rows may continue
+    the same pending row (``continue_pending`` refuses a request id given
+    twice). The plan arrays (source page,
     accepted length, final page, boundary page, boundary length; int32) and
     the records are those of the pending step, indexed by pending row, and
     cover ``num_rows`` rows. A next row applies its pending commit only when

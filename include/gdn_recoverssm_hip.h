@@ -162,7 +162,9 @@ int gdn_recoverssm_verify_gated(const void *q, const void *k, const void *v, con
  * length; see gdn_recoverssm_plan) are indexed by pending row and cover
  * `num_rows` (>= 1) rows. The records are the previous step's typed SoA planes
  * (or packed FP32 rows, key_per_value_head = 1); they must not be the buffers
- * the current verify writes. Strides in elements. */
+ * the current verify writes. No two current rows may continue the same
+ * pending row (two requests never share a state page): both would fold it
+ * into its final page. Strides in elements. */
 typedef struct gdn_pending_commit {
   const int32_t *rows;
   const int32_t *source;
