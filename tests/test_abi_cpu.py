@@ -240,6 +240,7 @@ def test_settle_is_checked_before_launch():
         (dict(groups=4), b"groups"),
         (dict(num_rows=9), b"pending rows"),
         (dict(num_rows=-1), b"pending rows"),
+        (dict(cap=N.SETTLE_MAX_ROWS + 8, num_rows=N.SETTLE_MAX_ROWS + 1), b"pending rows"),
         (dict(cap=0, num_rows=0), b"groups"),
         (dict(out=0), b"missing"),
         (dict(cnt=0), b"missing"),
