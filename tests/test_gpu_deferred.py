@@ -750,6 +750,80 @@ def test_flushes_and_settles_fold_each_row_once(dev):
         _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the flushes and settles")
 
 
+def test_deferred_step_graph_replay(dev):
+    """The start of a deferred step recorded in a HIP graph: a settle (one
+    continued row given another page, so it folds that row's commit through
+    the counted row list) and every layer's deferred verify. Three replays,
+    each from the same pages and plan with eager work in between, reproduce
+    the eager launches bit for bit: pages, outputs, records and the plan's
+    marks."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=49)
+    s = w.spec
+    L, B, Q, HV, V = s.layers, s.rows, s.window, s.value_heads, s.value_dim
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[::4] = 2
+    st = _first_step(w, dev, acc)
+    plan, ctx, ckpts, recs, pending = st["plan"], st["ctx"], st["ckpts"], st["recs"], st["pending"]
+    n, fin = plan["commit_lens"], plan["final"]
+    active = [r for r in range(B) if int(n[r]) > 0]
+    assert len(active) >= 2
+    moved = active[1]
+    pad = int(w.extras["padded_rows"][0])
+    free_page = next(int(p) for p in w.meta.block_table[pad].tolist() if 0 < int(p) < w.num_pages)
+    si = torch.where(n > 0, fin.to(torch.int32), w.meta.state_indices.to(torch.int32))
+    si[moved] = free_page
+    si_d = si.to(dev)
+    wd = w.to(dev)
+    qsl = wd.meta.query_start_loc
+    outs = [torch.empty(1, w.tokens, HV, V, dtype=wd.inputs[0].v.dtype, device=dev) for _ in range(L)]
+    print(f"deferred graph replay: row {moved} moves to page {free_page}", flush=True)
+
+    def run():
+        ctx.settle_deferred(si_d, pending[0].rows)
+        for layer in range(L):
+            gdn_recoverssm_verify_deferred(*_step_inputs(wd, layer, w.tokens), checkpoint_state=ckpts[layer],
+                                           replay_cache=recs[1][layer], pending=pending[layer],
+                                           query_start_loc=qsl, state_indices=si_d, spec_query_len=Q,
+                                           out=outs[layer])
+
+    pages0 = [c.clone() for c in ckpts]
+    lens0 = ctx.commit_lens.clone()
+
+    def reset():
+        for c, c0 in zip(ckpts, pages0):
+            c.copy_(c0)
+        ctx.commit_lens.copy_(lens0)
+        for t in outs + [x for r in recs[1] for x in (r.correction, r.key, r.decay)]:
+            t.fill_(-7.0)
+
+    def results():
+        return ([c.clone() for c in ckpts] + [o.clone() for o in outs] +
+                [x.clone() for r in recs[1] for x in (r.correction, r.key, r.decay)] + [ctx.commit_lens.clone()])
+
+    reset()
+    run()
+    torch.cuda.synchronize()
+    want = results()
+    assert int(ctx.commit_lens[moved]) == 0 and int(lens0[moved]) > 0, "the settle marks the row it folds"
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()  # warm the launch path on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for rep in range(3):
+        reset()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (got, ref) in enumerate(zip(results(), want)):
+            assert torch.equal(got, ref), f"replay {rep}: result {i} differs from the eager launches"
+
+
 def test_counted_row_list_folds_the_counted_rows(dev):
     """A fold with a device row count (gdn_fold_ext.row_count) folds the
     first `count` entries of its row list, clamped to the list: count 2 of a
