@@ -51,3 +51,35 @@ def test_row_map_random_batches(seed):
     want = [prev.index(req) if req in prev else -1 for req in nxt] or [-1]
     assert rows.tolist() == want
     assert left == sorted(r for r, req in enumerate(prev) if req not in nxt)
+
+
+def test_settle_spec_refuses_bad_arguments_on_the_host():
+    """The settle's launch is checked before it is built: 1-3 plan groups,
+    pending rows within the plan, an int32 row map covering the next batch,
+    1-D int32 / int64 next state indices on the plan's device."""
+    from gdn_recoverssm_ascend.kernels import _settle_spec
+
+    i32 = torch.int32
+    lengths, finals = torch.zeros(8, dtype=i32), torch.ones(8, dtype=i32)
+    out, rl, cnt = torch.zeros(8, dtype=i32), torch.zeros(8, dtype=i32), torch.zeros(1, dtype=i32)
+    rows, nxt = torch.arange(4, dtype=i32), torch.ones(4, dtype=i32)
+
+    def spec(**kw):
+        a = dict(lengths=lengths, finals=finals, capacity=8, num_rows=4, rows=rows, nexts=[nxt], out=out,
+                 row_list=rl, row_count=cnt)
+        a.update(kw)
+        return _settle_spec(a["lengths"], a["finals"], a["capacity"], a["num_rows"], a["rows"], a["nexts"], a["out"],
+                            a["row_list"], a["row_count"])
+
+    assert spec().name == "settle"
+    for kw, msg in [
+        (dict(nexts=[]), "plan groups"),
+        (dict(nexts=[nxt] * 4), "plan groups"),
+        (dict(num_rows=9), "pending rows"),
+        (dict(rows=rows.long()), "row map"),
+        (dict(rows=rows[:3]), "does not cover"),
+        (dict(nexts=[nxt.view(2, 2)]), "1-D int32 or int64"),
+        (dict(nexts=[nxt.float()]), "1-D int32 or int64"),
+    ]:
+        with pytest.raises(ValueError, match=msg):
+            spec(**kw)
