@@ -163,3 +163,47 @@ def test_deferred_commit_rejects_groups_on_other_rows(dev):
     one = torch.zeros(B + 1, dtype=torch.int32, device=dev)
     with pytest.raises(ValueError, match="GDN RecoverSSM: the deferred grouped commit needs every group on one"):
         GroupedCommitCoordinator().commit_deferred(metas, one[:B], one[:B], one, one.clone())
+
+
+def test_grouped_flushes_fold_each_row_once(dev):
+    """``DeferredGroupedCommit.flush`` marks what it folds in every bucket's
+    plan: a flush of one committed row, a flush of that row and another, then
+    a flush of everything fold each pending commit once, so every group's
+    pages equal the oracle's fold of the whole step."""
+    B, n_groups, seed = 6, 4, 730
+    gen = torch.Generator().manual_seed(seed)
+    request_rows = torch.randperm(B, generator=gen).tolist()
+    groups = _groups(B, n_groups, seed)
+    sampled = torch.zeros(B, dtype=torch.int32)
+    for b, r in enumerate(request_rows):
+        sampled[r] = max(1, int(groups[0]["acc"][b]))
+    metas, devs = [], []
+    for G in groups:
+        _index_by_request(G, request_rows)
+        ckpts, convs, recs = _to_dev(G, dev)
+        ctx = GDNRecoverSSMCommitContext.from_tensors(convs, ckpts, recs, spec_query_len=4, max_num_reqs=B)
+        devs.append((ckpts, convs))
+        metas.append(_entry(G, ctx, dev, request_rows).metadata)
+    mapping = torch.randperm(B + 2, generator=gen)[:B].to(torch.int32)
+    cols = torch.full((B + 2,), -9, dtype=torch.int32)
+    accp = torch.full((B + 2,), 7, dtype=torch.int32)
+    d = GroupedCommitCoordinator().commit_deferred(metas, sampled.to(dev), mapping.to(dev), cols.to(dev),
+                                                   accp.to(dev))
+    torch.cuda.synchronize()
+    want = _oracle_grouped(groups, sampled, mapping, cols, accp, request_rows, True, B)
+    committed = [b for b in range(B) if int(want["length"][b]) > 0]
+    assert len(committed) >= 2
+    print(f"grouped flushes: rows {committed[:2]}", flush=True)
+    d.flush(rows=[committed[0]])
+    d.flush(rows=committed[:2])
+    d.flush()
+    torch.cuda.synchronize()
+    for gi, G in enumerate(groups):
+        seg = slice(gi * B, gi * B + B)
+        assert int(d._plan(gi)[1][:B].abs().sum()) == 0, f"group {gi}: every pending row is marked folded"
+        corrs, keys, decays = _planes(G)
+        wstate = O.oracle_fold(G["ckpts"], corrs, keys, decays, source=want["source"][seg],
+                               lengths=want["length"][seg], final=want["final"][seg], boundary=want["boundary"][seg],
+                               boundary_len=want["boundary_len"][seg], rows=B, num_blocks=G["NB"], record_rows=B)
+        targeted = set(want["final"][seg].tolist()) | set(want["boundary"][seg].tolist())
+        _check_states(devs[gi][0], wstate, torch.float32, targeted)
