@@ -1182,9 +1182,10 @@ class GDNRecoverSSMCommitContext:
         after it, e.g. the end of a batch); a list of pending rows folds only
         those (rows whose request left the batch, see ``continue_pending``),
         leaving the rest to the next verify. The folded rows are then marked
-        in the plan (accepted length 0), so a later flush or settle does not
-        fold them again; a row the next verify has applied is not marked
-        (every layer's verify reads the plan), so it must not be flushed.
+        in the plan (accepted length 0), so a later flush, settle or verify
+        does not apply them again (a verify then reads the folded final
+        page); a row the next verify has applied is not marked (every layer's
+        verify reads the plan), so it must not be flushed afterwards.
         """
         spec = getattr(self, "_deferred_fold", None)
         require(spec is not None, "no deferred commit to flush")

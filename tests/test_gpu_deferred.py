@@ -750,6 +750,49 @@ def test_flushes_and_settles_fold_each_row_once(dev):
         _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the flushes and settles")
 
 
+def test_a_flushed_row_is_not_applied_again_by_the_verify(dev):
+    """A row flushed before the next verify (its request continues on its
+    final page) is marked folded, so that verify reads the folded final page
+    instead of applying the commit a second time: after the flush of two
+    continuing rows and every layer's deferred verify, the pages equal the
+    oracle's fold of the whole step (each commit once) and the outputs equal
+    the oracle's verify from those pages."""
+    w = W.make_workload("decode_loop_l48", layers=2, rows=12, key_heads=2, value_heads=4, key_dim=128, value_dim=128,
+                        steps=2, max_position=512, block_size=8, padded_rows=1, seed=53)
+    s = w.spec
+    L, B, Q = s.layers, s.rows, s.window
+    acc = torch.full((B,), Q, dtype=torch.int32)
+    acc[2::5] = 1
+    st = _first_step(w, dev, acc)
+    plan, ctx, ckpts, recs, pending = st["plan"], st["ctx"], st["ckpts"], st["recs"], st["pending"]
+    n, fin = plan["commit_lens"], plan["final"]
+    active = [r for r in range(B) if int(n[r]) > 0]
+    assert len(active) >= 4
+    flushed = [active[1], active[3]]
+    print(f"flush before the verify: rows {flushed}", flush=True)
+    before = [x.cpu() for x in w.checkpoints]
+    ctx.flush_deferred(rows=flushed)
+    idx1 = torch.where(n > 0, fin.to(torch.int32), w.meta.state_indices.to(torch.int32))
+    gen = torch.Generator().manual_seed(54)
+    inputs1 = [W.make_layer_inputs(s, B * Q, gen) for _ in range(L)]
+    qd, idx_d = w.meta.query_start_loc.to(dev), idx1.to(dev)
+    outs = []
+    for layer in range(L):
+        i = inputs1[layer]
+        outs.append(gdn_recoverssm_verify_deferred(
+            i.g.to(dev), i.beta.to(dev), i.q.to(dev), i.k.to(dev), i.v.to(dev), checkpoint_state=ckpts[layer],
+            replay_cache=recs[1][layer], pending=pending[layer], query_start_loc=qd, state_indices=idx_d,
+            spec_query_len=Q))
+    torch.cuda.synchronize()
+    want = _oracle_fold(before, st["results"], plan, B, w.num_pages)
+    touched = _touched(plan, B, w.num_pages)
+    for layer in range(L):
+        _check_pages(ckpts[layer], want[layer], touched, f"layer {layer}: pages after the flush and the verify")
+        i = inputs1[layer]
+        r1 = O.oracle_verify(i.q, i.k, i.v, i.g, i.beta, want[layer], w.meta.query_start_loc, idx1, Q)
+        _check_verify(outs[layer], recs[1][layer], r1, f"step 1 layer {layer}")
+
+
 def test_deferred_step_graph_replay(dev):
     """The start of a deferred step recorded in a HIP graph: a settle (one
     continued row given another page, so it folds that row's commit through
